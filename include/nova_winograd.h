@@ -1,0 +1,130 @@
+/*
+ * libnova_winograd.so -- C-ABI of the MI355X-native NOVA F(6,3) Winograd
+ * convolution (3x3, stride 1, fp16 activations, fp32 weights).
+ *
+ * Every symbol the reference's ctypes bridge binds
+ * (/root/reference/nova_winograd/ops.py:66-114) is declared here with the
+ * reference's exact C signature (/root/reference/csrc/nova_winograd.hip:679-758),
+ * so the reference's Python package, or any ctypes/cffi/C caller written
+ * against it, binds this library unchanged. Extensions follow, each marked.
+ *
+ * Conventions (same as the reference):
+ *   - all data pointers are device pointers owned by the caller;
+ *   - x is fp16 NCHW [B][C][H][W], contiguous; w is fp32 [K][C][3][3];
+ *     y is fp16 NCHW [B][K][Ho][Wo] with Ho = H + 2*pad - 2;
+ *   - functions return void; failures no longer exit the process (the
+ *     reference calls exit(1)): they leave the output untouched, record a
+ *     code and message, and nova_get_last_error() reports them.
+ * Streams: work of a handle goes to the stream set with nova_set_stream()
+ * (default: the null stream, as in the reference). Handle-less entry points
+ * (nova_filter_transform, nova_input_transform, nova_output_transform) use
+ * the null stream, as in the reference.
+ */
+#ifndef NOVA_WINOGRAD_H
+#define NOVA_WINOGRAD_H
+
+#if defined(__GNUC__)
+#define NOVA_API __attribute__((visibility("default")))
+#else
+#define NOVA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* nova_handle_t;
+
+/* ---- Reference C-ABI (12 symbols) ---------------------------------------- */
+
+/* Replaces nova_create, /root/reference/csrc/nova_winograd.hip:686-690.
+ * No device work: the transform tables are compiled into the kernels. */
+NOVA_API nova_handle_t nova_create(void);
+
+/* Replaces nova_destroy, /root/reference/csrc/nova_winograd.hip:692-694.
+ * Frees the handle's filter transform and workspace; NULL is a no-op. */
+NOVA_API void nova_destroy(nova_handle_t h);
+
+/* Replaces nova_set_weights, /root/reference/csrc/nova_winograd.hip:696-698.
+ * Transforms fp32 w[K][C][3][3] into the handle's Winograd-domain filter
+ * (asynchronous on the handle's stream). */
+NOVA_API void nova_set_weights(nova_handle_t h, const void* d_weight, int K, int C);
+
+/* Replaces nova_forward, /root/reference/csrc/nova_winograd.hip:700-706.
+ * Uses a handle-owned, grow-only workspace (the reference mallocs and frees
+ * per call). */
+NOVA_API void nova_forward(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
+                  int W, int pad);
+
+/* Replaces nova_forward_workspace, /root/reference/csrc/nova_winograd.hip:708-717.
+ * d_V_gemm / d_M_gemm are caller workspaces of at least 64*C*BP and 64*K*BP
+ * fp16 elements, BP = batch*nh*nw with (nh, nw) from nova_compute_tiling.
+ * They are used when large enough for the internal layout, otherwise the
+ * handle's own workspace is used; their contents afterwards are unspecified. */
+NOVA_API void nova_forward_workspace(nova_handle_t h, const void* d_input, void* d_output,
+                            void* d_V_gemm, void* d_M_gemm, int batch, int H, int W, int pad,
+                            int nh, int nw);
+
+/* Replaces nova_compute_tiling, /root/reference/csrc/nova_winograd.hip:719-721
+ * (law :617-631): Ho = H+2p-2; nh = ceil((Ho-1)/6)+1. Host-only, no device. */
+NOVA_API void nova_compute_tiling(int H, int W, int pad, int* nh, int* nw, int* H_out, int* W_out);
+
+/* Replaces nova_filter_transform, /root/reference/csrc/nova_winograd.hip:724-728.
+ * Writes U in the reference layout U[p*K*C + c*K + k] and synchronizes. */
+NOVA_API void nova_filter_transform(const void* d_weight, void* d_U_gemm, int K, int C);
+
+/* Replaces nova_input_transform, /root/reference/csrc/nova_winograd.hip:731-739.
+ * Writes V in the reference layout V[p*C*BP + bp*C + c], bp = b*nh*nw + tile. */
+NOVA_API void nova_input_transform(const void* d_input, void* d_V_gemm, int batch, int C, int H, int W,
+                          int pad, int nh, int nw, int BP);
+
+/* Replaces nova_output_transform, /root/reference/csrc/nova_winograd.hip:742-750.
+ * Reads M in the reference layout M[p*K*BP + bp*K + k]. */
+NOVA_API void nova_output_transform(const void* d_M_gemm, void* d_output, int batch, int K, int H_out,
+                           int W_out, int nh, int nw, int BP);
+
+/* Replace nova_get_K / nova_get_C / nova_get_U_gemm,
+ * /root/reference/csrc/nova_winograd.hip:752-754. The U pointer refers to
+ * this library's layout U[p][k][Cp] (Cp = C rounded up to 8, zero padded). */
+NOVA_API int nova_get_K(nova_handle_t h);
+NOVA_API int nova_get_C(nova_handle_t h);
+NOVA_API void* nova_get_U_gemm(nova_handle_t h);
+
+/* ---- Reference fused C-API (declared in the reference, never bound) ------ */
+/* Replace nova_fused_create/destroy/set_weights/forward/compute_tiling,
+ * /root/reference/csrc/nova_winograd_fused.hip:619-652. They are the same
+ * handle as above; the fused/3-pass choice is made per call. */
+NOVA_API nova_handle_t nova_fused_create(void);
+NOVA_API void nova_fused_destroy(nova_handle_t h);
+NOVA_API void nova_fused_set_weights(nova_handle_t h, const void* d_weight, int K, int C);
+NOVA_API void nova_fused_forward(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
+                        int W, int pad);
+NOVA_API void nova_fused_compute_tiling(int H, int W, int pad, int* nh, int* nw, int* H_out, int* W_out);
+
+/* ---- Extensions (no reference counterpart) ------------------------------- */
+
+/* Last error of the calling thread: returns the code (0 = none) and clears it. */
+NOVA_API int nova_get_last_error(void);
+/* Message for the calling thread's most recent error ("" if none). */
+NOVA_API const char* nova_get_last_error_message(void);
+
+/* Stream for the handle's subsequent work (a hipStream_t; NULL = null stream). */
+NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
+
+/* Path selection: 0 = automatic (default), 1 = force 3-pass, 2 = force fused
+ * (falls back to 3-pass with an error if the shape is unsupported). */
+NOVA_API void nova_set_path(nova_handle_t h, int path);
+/* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused. */
+NOVA_API int nova_get_last_path(nova_handle_t h);
+
+/* Internal workspace bytes a forward of this shape needs on this handle. */
+NOVA_API long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad);
+
+/* Library version string. */
+NOVA_API const char* nova_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NOVA_WINOGRAD_H */

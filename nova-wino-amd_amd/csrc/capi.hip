@@ -1,0 +1,394 @@
+// C-ABI of libnova_winograd.so and the per-handle host runtime.
+//
+// The handle replaces the reference's NovaWinogradF63 / NovaWinogradFused
+// host classes (/root/reference/csrc/nova_winograd.hip:456-611,
+// /root/reference/csrc/nova_winograd_fused.hip:446-607): it owns the
+// Winograd-domain filter U (product layout [64][K][Cp]) and a grow-only
+// workspace, launches on a caller-selected stream, and picks the fused or the
+// 3-pass pipeline per call. Errors are recorded per thread instead of exiting
+// the process.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/nova_winograd.h"
+#include "nova_internal.h"
+
+namespace nova {
+
+static thread_local int g_err = 0;
+static thread_local char g_msg[512] = "";
+
+void set_error(int code, const char* fmt, ...) {
+    g_err = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+    va_end(ap);
+}
+
+namespace {
+
+constexpr uint32_t kMagic = 0x4e4f5641u;  // "NOVA"
+
+struct Handle {
+    uint32_t magic = kMagic;
+    int K = 0, C = 0, Cp = 0;
+    uint16_t* U = nullptr;
+    size_t U_cap = 0;  // bytes
+    void* ws = nullptr;
+    size_t ws_cap = 0;  // bytes
+    hipStream_t stream = nullptr;
+    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused
+    int last_path = 0;
+    bool ready = false;
+};
+
+Handle* as_handle(nova_handle_t h, const char* fn) {
+    Handle* H = static_cast<Handle*>(h);
+    if (H == nullptr || H->magic != kMagic) {
+        set_error(kErrInvalidArgument, "%s: invalid handle", fn);
+        return nullptr;
+    }
+    return H;
+}
+
+bool hip_ok(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    set_error(e == hipErrorOutOfMemory ? kErrOutOfMemory : kErrHip, "%s: %s", what,
+              hipGetErrorString(e));
+    return false;
+}
+
+void reference_tiling(int H, int W, int pad, int* nh, int* nw, int* Ho, int* Wo) {
+    // /root/reference/csrc/nova_winograd.hip:617-631: pad the output extent
+    // by n-1 = 7 and round (extent - 8) up to a multiple of 6.
+    const int m = 6, n = 8;
+    *Ho = H + 2 * pad - 2;
+    *Wo = W + 2 * pad - 2;
+    int hp = *Ho + n - 1, wp = *Wo + n - 1;
+    hp += (m - (hp - n) % m) % m;
+    wp += (m - (wp - n) % m) % m;
+    *nh = (hp - n) / m + 1;
+    *nw = (wp - n) / m + 1;
+}
+
+bool ensure_ws(Handle* H, size_t bytes) {
+    if (bytes <= H->ws_cap) return true;
+    if (H->ws) {
+        if (!hip_ok(hipFree(H->ws), "hipFree(workspace)")) return false;
+        H->ws = nullptr;
+        H->ws_cap = 0;
+    }
+    // 25% headroom so that slowly growing batches do not reallocate each call
+    const size_t want = bytes + bytes / 4;
+    if (!hip_ok(hipMalloc(&H->ws, want), "hipMalloc(workspace)")) return false;
+    H->ws_cap = want;
+    return true;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct Shape {
+    int B, H, W, pad, Ho, Wo, nh, nw;
+    int64_t BP;
+};
+
+bool make_shape(const Handle* Hd, int B, int H, int W, int pad, Shape* s, const char* fn) {
+    if (B < 0 || H < 1 || W < 1 || pad < 0) {
+        set_error(kErrInvalidArgument, "%s: bad shape B=%d H=%d W=%d pad=%d", fn, B, H, W, pad);
+        return false;
+    }
+    s->B = B;
+    s->H = H;
+    s->W = W;
+    s->pad = pad;
+    s->Ho = H + 2 * pad - 2;
+    s->Wo = W + 2 * pad - 2;
+    if (s->Ho < 1 || s->Wo < 1) {
+        set_error(kErrInvalidArgument, "%s: empty output for H=%d W=%d pad=%d", fn, H, W, pad);
+        return false;
+    }
+    s->nh = tiles_min(s->Ho);
+    s->nw = tiles_min(s->Wo);
+    s->BP = (int64_t)B * s->nh * s->nw;
+    const int cblocks = (Hd->Cp + 63) / 64, kblocks = (Hd->K + 63) / 64;
+    if (s->nh > 65535 || (int64_t)B * cblocks > 65535 || (int64_t)B * kblocks > 65535 ||
+        s->BP > (int64_t)1 << 30) {
+        set_error(kErrInvalidArgument, "%s: shape exceeds launch limits", fn);
+        return false;
+    }
+    return true;
+}
+
+bool use_fused(const Handle* Hd, const Shape& s) {
+    if (!fused_supported(Hd->K, Hd->C)) return false;
+    if (Hd->path_pref == 2) return true;
+    if (Hd->path_pref == 1) return false;
+    // Automatic choice: the fused kernel wins when V/M round trips through
+    // memory dominate, i.e. for small channel counts.
+    return Hd->K <= 64 && Hd->C <= 64;
+    (void)s;
+}
+
+// Core forward. V_user/M_user may be null; caps are in fp16 elements.
+void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s, void* V_user,
+                  int64_t V_cap, void* M_user, int64_t M_cap, const char* fn) {
+    if (!Hd->ready) {
+        set_error(kErrNotInitialized, "%s: call nova_set_weights() before forward", fn);
+        return;
+    }
+    if (x == nullptr || y == nullptr) {
+        set_error(kErrInvalidArgument, "%s: null input or output pointer", fn);
+        return;
+    }
+    if (s.B == 0) return;
+    const uint16_t* xx = static_cast<const uint16_t*>(x);
+    uint16_t* yy = static_cast<uint16_t*>(y);
+
+    if (use_fused(Hd, s)) {
+        Hd->last_path = 2;
+        hip_ok(launch_fused(xx, Hd->U, yy, s.B, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.pad, s.nh, s.nw,
+                            s.Ho, s.Wo, Hd->stream),
+               "fused kernel");
+        return;
+    }
+    if (Hd->path_pref == 2) {
+        set_error(kErrInvalidArgument, "%s: fused path unsupported for K=%d C=%d; ran 3-pass", fn,
+                  Hd->K, Hd->C);
+    }
+    Hd->last_path = 1;
+    const int64_t needV = 64 * (int64_t)Hd->Cp * s.BP;
+    const int64_t needM = 64 * (int64_t)Hd->K * s.BP;
+    uint16_t* V = nullptr;
+    uint16_t* M = nullptr;
+    size_t ws_bytes = 0;
+    const bool userV = V_user && needV <= V_cap && aligned16(V_user);
+    const bool userM = M_user && needM <= M_cap && aligned16(M_user);
+    if (!userV) ws_bytes += (size_t)needV * 2;
+    if (!userM) ws_bytes += (size_t)needM * 2;
+    if (ws_bytes && !ensure_ws(Hd, ws_bytes)) return;
+    uint8_t* wsp = static_cast<uint8_t*>(Hd->ws);
+    if (userV) {
+        V = static_cast<uint16_t*>(V_user);
+    } else {
+        V = reinterpret_cast<uint16_t*>(wsp);
+        wsp += (size_t)needV * 2;
+    }
+    M = userM ? static_cast<uint16_t*>(M_user) : reinterpret_cast<uint16_t*>(wsp);
+
+    if (!hip_ok(launch_input_transform(xx, V, s.B, Hd->C, s.H, s.W, s.pad, s.nh, s.nw, Hd->Cp,
+                                       (int64_t)Hd->Cp * s.BP, Hd->stream),
+                "input transform"))
+        return;
+    if (!hip_ok(launch_wgemm(Hd->U, V, M, Hd->K, Hd->Cp, (int)s.BP, Hd->stream), "wgemm"))
+        return;
+    hip_ok(launch_output_transform(M, yy, s.B, Hd->K, s.Ho, s.Wo, s.nh, s.nw, Hd->K,
+                                   (int64_t)Hd->K * s.BP, Hd->stream),
+           "output transform");
+}
+
+}  // namespace
+}  // namespace nova
+
+using namespace nova;
+
+extern "C" {
+
+nova_handle_t nova_create(void) {
+    Handle* H = new (std::nothrow) Handle();
+    if (!H) set_error(kErrOutOfMemory, "nova_create: out of host memory");
+    return H;
+}
+
+void nova_destroy(nova_handle_t h) {
+    if (h == nullptr) return;
+    Handle* H = as_handle(h, "nova_destroy");
+    if (!H) return;
+    if (H->U) hip_ok(hipFree(H->U), "hipFree(U)");
+    if (H->ws) hip_ok(hipFree(H->ws), "hipFree(workspace)");
+    H->magic = 0;
+    delete H;
+}
+
+void nova_set_weights(nova_handle_t h, const void* d_weight, int K, int C) {
+    Handle* H = as_handle(h, "nova_set_weights");
+    if (!H) return;
+    if (d_weight == nullptr || K < 1 || C < 1) {
+        set_error(kErrInvalidArgument, "nova_set_weights: bad arguments (w=%p K=%d C=%d)",
+                  d_weight, K, C);
+        return;
+    }
+    const int Cp = pad8(C);
+    const size_t need = (size_t)64 * K * Cp * sizeof(uint16_t);
+    if (need > H->U_cap) {
+        if (H->U) {
+            if (!hip_ok(hipFree(H->U), "hipFree(U)")) return;
+            H->U = nullptr;
+            H->U_cap = 0;
+        }
+        if (!hip_ok(hipMalloc(&H->U, need), "hipMalloc(U)")) {
+            H->ready = false;
+            return;
+        }
+        H->U_cap = need;
+    }
+    H->K = K;
+    H->C = C;
+    H->Cp = Cp;
+    H->ready = hip_ok(launch_filter_transform_gemm(static_cast<const float*>(d_weight), H->U, K,
+                                                   C, Cp, H->stream),
+                      "filter transform");
+}
+
+void nova_forward(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
+                  int W, int pad) {
+    Handle* Hd = as_handle(h, "nova_forward");
+    if (!Hd) return;
+    Shape s;
+    if (!make_shape(Hd, batch, H, W, pad, &s, "nova_forward")) return;
+    forward_impl(Hd, d_input, d_output, s, nullptr, 0, nullptr, 0, "nova_forward");
+}
+
+void nova_forward_workspace(nova_handle_t h, const void* d_input, void* d_output,
+                            void* d_V_gemm, void* d_M_gemm, int batch, int H, int W, int pad,
+                            int nh, int nw) {
+    Handle* Hd = as_handle(h, "nova_forward_workspace");
+    if (!Hd) return;
+    Shape s;
+    if (!make_shape(Hd, batch, H, W, pad, &s, "nova_forward_workspace")) return;
+    if (nh < s.nh || nw < s.nw) {
+        set_error(kErrWorkspace,
+                  "nova_forward_workspace: tiling %dx%d does not cover the %dx%d output", nh, nw,
+                  s.Ho, s.Wo);
+        return;
+    }
+    const int64_t bp_user = (int64_t)batch * nh * nw;
+    forward_impl(Hd, d_input, d_output, s, d_V_gemm, 64 * (int64_t)Hd->C * bp_user, d_M_gemm,
+                 64 * (int64_t)Hd->K * bp_user, "nova_forward_workspace");
+}
+
+void nova_compute_tiling(int H, int W, int pad, int* nh, int* nw, int* H_out, int* W_out) {
+    if (!nh || !nw || !H_out || !W_out) {
+        set_error(kErrInvalidArgument, "nova_compute_tiling: null output pointer");
+        return;
+    }
+    reference_tiling(H, W, pad, nh, nw, H_out, W_out);
+}
+
+void nova_filter_transform(const void* d_weight, void* d_U_gemm, int K, int C) {
+    if (!d_weight || !d_U_gemm || K < 1 || C < 1) {
+        set_error(kErrInvalidArgument, "nova_filter_transform: bad arguments");
+        return;
+    }
+    if (!hip_ok(launch_filter_transform_ref(static_cast<const float*>(d_weight),
+                                            static_cast<uint16_t*>(d_U_gemm), K, C, nullptr),
+                "filter transform"))
+        return;
+    hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+}
+
+void nova_input_transform(const void* d_input, void* d_V_gemm, int batch, int C, int H, int W,
+                          int pad, int nh, int nw, int BP) {
+    if (!d_input || !d_V_gemm || batch < 0 || C < 1 || H < 1 || W < 1 || pad < 0 || nh < 1 ||
+        nw < 1 || (int64_t)BP < (int64_t)batch * nh * nw) {
+        set_error(kErrInvalidArgument, "nova_input_transform: bad arguments");
+        return;
+    }
+    if (batch == 0) return;
+    if (nh > 65535 || (int64_t)batch * ((C + 63) / 64) > 65535) {
+        set_error(kErrInvalidArgument, "nova_input_transform: shape exceeds launch limits");
+        return;
+    }
+    hip_ok(launch_input_transform(static_cast<const uint16_t*>(d_input),
+                                  static_cast<uint16_t*>(d_V_gemm), batch, C, H, W, pad, nh, nw, C,
+                                  (int64_t)C * BP, nullptr),
+           "input transform");
+}
+
+void nova_output_transform(const void* d_M_gemm, void* d_output, int batch, int K, int H_out,
+                           int W_out, int nh, int nw, int BP) {
+    if (!d_M_gemm || !d_output || batch < 0 || K < 1 || H_out < 1 || W_out < 1 || nh < 1 ||
+        nw < 1 || (int64_t)BP < (int64_t)batch * nh * nw) {
+        set_error(kErrInvalidArgument, "nova_output_transform: bad arguments");
+        return;
+    }
+    if (batch == 0) return;
+    if (nh > 65535 || (int64_t)batch * ((K + 63) / 64) > 65535) {
+        set_error(kErrInvalidArgument, "nova_output_transform: shape exceeds launch limits");
+        return;
+    }
+    hip_ok(launch_output_transform(static_cast<const uint16_t*>(d_M_gemm),
+                                   static_cast<uint16_t*>(d_output), batch, K, H_out, W_out, nh,
+                                   nw, K, (int64_t)K * BP, nullptr),
+           "output transform");
+}
+
+int nova_get_K(nova_handle_t h) {
+    Handle* H = as_handle(h, "nova_get_K");
+    return H ? H->K : 0;
+}
+
+int nova_get_C(nova_handle_t h) {
+    Handle* H = as_handle(h, "nova_get_C");
+    return H ? H->C : 0;
+}
+
+void* nova_get_U_gemm(nova_handle_t h) {
+    Handle* H = as_handle(h, "nova_get_U_gemm");
+    return H ? H->U : nullptr;
+}
+
+nova_handle_t nova_fused_create(void) { return nova_create(); }
+void nova_fused_destroy(nova_handle_t h) { nova_destroy(h); }
+void nova_fused_set_weights(nova_handle_t h, const void* d_weight, int K, int C) {
+    nova_set_weights(h, d_weight, K, C);
+}
+void nova_fused_forward(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
+                        int W, int pad) {
+    nova_forward(h, d_input, d_output, batch, H, W, pad);
+}
+void nova_fused_compute_tiling(int H, int W, int pad, int* nh, int* nw, int* H_out, int* W_out) {
+    nova_compute_tiling(H, W, pad, nh, nw, H_out, W_out);
+}
+
+int nova_get_last_error(void) {
+    const int e = g_err;
+    g_err = 0;
+    return e;
+}
+
+const char* nova_get_last_error_message(void) { return g_msg; }
+
+void nova_set_stream(nova_handle_t h, void* stream) {
+    Handle* H = as_handle(h, "nova_set_stream");
+    if (H) H->stream = static_cast<hipStream_t>(stream);
+}
+
+void nova_set_path(nova_handle_t h, int path) {
+    Handle* H = as_handle(h, "nova_set_path");
+    if (!H) return;
+    if (path < 0 || path > 2) {
+        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1 or 2");
+        return;
+    }
+    H->path_pref = path;
+}
+
+int nova_get_last_path(nova_handle_t h) {
+    Handle* H = as_handle(h, "nova_get_last_path");
+    return H ? H->last_path : 0;
+}
+
+long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad) {
+    Handle* Hd = as_handle(h, "nova_workspace_bytes");
+    if (!Hd) return -1;
+    Shape s;
+    if (!make_shape(Hd, batch, H, W, pad, &s, "nova_workspace_bytes")) return -1;
+    if (Hd->ready && use_fused(Hd, s)) return 0;
+    return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * s.BP * 2);
+}
+
+const char* nova_version(void) { return "nova-winograd-mi355x 0.1.0 (gfx950)"; }
+
+}  // extern "C"

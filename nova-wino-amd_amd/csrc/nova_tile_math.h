@@ -1,0 +1,106 @@
+// Per-tile NOVA F(6,3) transform arithmetic, shared by the standalone
+// transform kernels and the fused kernel.
+//
+// Order of operations (the contract the CPU oracle restates):
+//   input : t[r][j] = fma-chain_i  Bh[i][r] * d[i][j]        (i = 0..7)
+//           v[r][s] = fma-chain_j  t[r][j]  * Bh[j][s]        (j = 0..7)
+//   output: t[r][j] = fma-chain_i  Ah[r][i] * m[i][j]         (r < 6)
+//           y[r][s] = fma-chain_j  t[r][j]  * Ah[s][j]        (s < 6)
+//   filter: u[r][s] = fma-chain_{p,q} (G[r][p]*w[p][q]) * G[s][q]
+// Chains start at +0 and skip terms whose table coefficient is zero (input
+// and output only). Loops are fully unrolled so that the constexpr tables fold
+// into immediates and the zero tests disappear at compile time.
+#pragma once
+
+#include "nova_tables.h"
+
+namespace nova {
+
+// Round an fp32 value to fp16 (nearest even) *as an fp32 value*. The empty asm
+// pins v in a register, which stops the compiler from fusing the producing
+// fma with the conversion into v_fma_mix{lo,hi}_f16 -- that instruction rounds
+// the exact fma result straight to fp16 (one rounding) and differs from
+// fp32-then-fp16 when the fp32 result lands on an fp16 tie.
+__device__ __forceinline__ _Float16 to_f16(float v) {
+    asm("" : "+v"(v));
+    return (_Float16)v;
+}
+
+// Input tile: ld(i, j) returns d[i][j] as fp32. Processes one input column j
+// at a time, which keeps every v[r][s] chain in j order.
+template <typename Load>
+__device__ __forceinline__ void input_tile(Load ld, float v[8][8]) {
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int s = 0; s < 8; s++) v[r][s] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float d[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) d[i] = ld(i, j);
+        float t[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], d[i], acc);
+            t[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                if (kBh[j][s] != 0.0f) v[r][s] = __builtin_fmaf(t[r], kBh[j][s], v[r][s]);
+    }
+}
+
+// Output tile: ld(i, j) returns m[i][j] (position 8*i+j) as fp32.
+template <typename Load>
+__device__ __forceinline__ void output_tile(Load ld, float y[6][6]) {
+#pragma unroll
+    for (int r = 0; r < 6; r++)
+#pragma unroll
+        for (int s = 0; s < 6; s++) y[r][s] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float m[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) m[i] = ld(i, j);
+        float t[6];
+#pragma unroll
+        for (int r = 0; r < 6; r++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (kAh[r][i] != 0.0f) acc = __builtin_fmaf(kAh[r][i], m[i], acc);
+            t[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 6; r++)
+#pragma unroll
+            for (int s = 0; s < 6; s++)
+                if (kAh[s][j] != 0.0f) y[r][s] = __builtin_fmaf(t[r], kAh[s][j], y[r][s]);
+    }
+}
+
+// Filter tile: all 9 terms, t = G[r][p]*w[p][q] rounded to fp32 first.
+__device__ __forceinline__ void filter_tile(const float w[3][3], float u[8][8]) {
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+#pragma unroll
+                for (int q = 0; q < 3; q++) {
+                    const float t = kG[r][p] * w[p][q];
+                    acc = __builtin_fmaf(t, kG[s][q], acc);
+                }
+            u[r][s] = acc;
+        }
+}
+
+}  // namespace nova

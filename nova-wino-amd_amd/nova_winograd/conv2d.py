@@ -1,0 +1,422 @@
+"""NOVA Winograd Conv2d modules -- drop-in replacements for ``torch.nn.Conv2d``
+(3x3, stride 1), mirroring /root/reference/nova_winograd/conv2d.py.
+
+Classes:
+    NovaWinogradConv2d           inference module: cached filter transform,
+                                 weight versioning, workspace caching
+    NovaWinogradConv2dTrainable  HIP forward, fp32 backward
+    NovaWinogradConv2dCompilable ``torch.compile`` through the custom op
+                                 ``torch.ops.nova.winograd_conv2d``
+
+The forward runs on the gfx950 library through the C-ABI; there is no CPU
+fallback (a CPU input raises).
+"""
+
+import atexit
+import math
+import threading
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from nova_winograd.ops import (
+    check,
+    compute_tiling,
+    current_stream_ptr,
+    get_lib,
+    ptr,
+    require_gpu_tensor,
+)
+
+
+def _weight_key(weight):
+    """Identity of the weight contents the cached filter transform was built
+    from. ``_version`` catches in-place updates (optimizer steps,
+    ``load_state_dict``); object identity, pointer, dtype and shape catch
+    re-binding, ``.to()`` and ``.half()``. (The reference keys on ``_version``
+    alone, /root/reference/nova_winograd/conv2d.py:195-203.)"""
+    return (id(weight), weight._version, weight.data_ptr(), weight.dtype,
+            tuple(weight.shape), weight.device)
+
+
+_exiting = False
+
+
+def _mark_exiting():
+    global _exiting
+    _exiting = True
+
+
+atexit.register(_mark_exiting)
+
+
+class _Handle:
+    """Owns one library handle; destroyed with the Python object (at
+    interpreter exit the process releases device memory itself)."""
+
+    __slots__ = ("h", "lib", "stream", "key")
+
+    def __init__(self):
+        self.lib = get_lib()
+        self.h = self.lib.nova_create()
+        check("create")
+        self.stream = 0
+        self.key = None
+
+    def set_stream(self, device):
+        s = current_stream_ptr(device)
+        if s != self.stream:
+            self.lib.nova_set_stream(self.h, s)
+            self.stream = s
+
+    def set_weights(self, weight):
+        # fp32 contiguous copy at the boundary: the library reads fp32
+        # [K,C,3,3]; the conversion also makes a .half()'d module safe. The
+        # temporary stays valid for the asynchronous transform because both
+        # run on the current stream (the caching allocator is stream-ordered).
+        w32 = weight.detach().to(torch.float32).contiguous()
+        self.lib.nova_set_weights(self.h, ptr(w32), w32.shape[0], w32.shape[1])
+        check("set_weights")
+
+    def __del__(self):
+        try:
+            if self.h and not _exiting:
+                self.lib.nova_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+# ─────────────────────────────────────────────────────────────────────────
+# torch.compile custom op (/root/reference/nova_winograd/conv2d.py:25-85)
+# ─────────────────────────────────────────────────────────────────────────
+
+_custom_op_registered = False
+_op_lock = threading.Lock()
+_OP_HANDLES = {}  # device index -> _Handle
+
+
+def _op_handle(device):
+    """One persistent handle per device for the custom op. The op receives
+    bare tensors (possibly temporaries), so their identity cannot key a
+    filter-transform cache safely: the filter is re-transformed on every call,
+    as the reference's op does (it also creates and destroys a handle and
+    synchronises twice per call)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    hd = _OP_HANDLES.get(idx)
+    if hd is None:
+        hd = _Handle()
+        _OP_HANDLES[idx] = hd
+    return hd
+
+
+def _grad_input(go, weight, padding, dtype):
+    return F.conv_transpose2d(go.float(), weight.float(), padding=padding).to(dtype)
+
+
+def _grad_weight(inp, go, weight, padding):
+    # One batched fp32 correlation instead of the reference's per-sample
+    # unfold loop (/root/reference/nova_winograd/conv2d.py:138-143).
+    gw = torch.nn.grad.conv2d_weight(inp.float(), tuple(weight.shape), go.float(),
+                                     padding=padding)
+    return gw.to(weight.dtype)
+
+
+def _register_custom_op():
+    """Register ``nova::winograd_conv2d`` as a torch.library custom op."""
+    global _custom_op_registered
+    with _op_lock:
+        if _custom_op_registered:
+            return
+        _custom_op_registered = True
+
+    @torch.library.custom_op("nova::winograd_conv2d", mutates_args=())
+    def nova_winograd_conv2d(input: torch.Tensor, weight: torch.Tensor,
+                             padding: int) -> torch.Tensor:
+        require_gpu_tensor(input, "input")
+        x = input.half().contiguous() if input.dtype != torch.float16 else input.contiguous()
+        w = weight.float().contiguous() if weight.dtype != torch.float32 else weight.contiguous()
+        B, C, H, W = x.shape
+        K = w.shape[0]
+        _, _, H_out, W_out = compute_tiling(H, W, padding)
+        output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=x.device)
+        with _op_lock:
+            hd = _op_handle(x.device)
+            hd.set_stream(x.device)
+            hd.set_weights(w)
+            hd.lib.nova_forward(hd.h, ptr(x), ptr(output), B, H, W, padding)
+            check("forward")
+        return output
+
+    @nova_winograd_conv2d.register_fake
+    def _(input, weight, padding):
+        B, C, H, W = input.shape
+        K = weight.shape[0]
+        return input.new_empty(B, K, H + 2 * padding - 2, W + 2 * padding - 2,
+                               dtype=torch.float16)
+
+    def _setup_context(ctx, inputs, output):
+        input, weight, padding = inputs
+        ctx.save_for_backward(input, weight)
+        ctx.padding = padding
+
+    def _backward(ctx, grad_output):
+        input, weight = ctx.saved_tensors
+        go = grad_output.contiguous()
+        gi = _grad_input(go, weight, ctx.padding, input.dtype)
+        gw = _grad_weight(input, go, weight, ctx.padding)
+        return gi, gw, None
+
+    nova_winograd_conv2d.register_autograd(_backward, setup_context=_setup_context)
+
+
+# ─────────────────────────────────────────────────────────────────────────
+# Autograd Function (/root/reference/nova_winograd/conv2d.py:92-147)
+# ─────────────────────────────────────────────────────────────────────────
+
+class NovaWinogradFunction(torch.autograd.Function):
+    """HIP forward, fp32 backward."""
+
+    @staticmethod
+    def forward(ctx, input, weight, bias, padding, handle_holder):
+        ctx.save_for_backward(input, weight, bias)
+        ctx.padding = padding
+        x = input.half().contiguous() if input.dtype != torch.float16 else input.contiguous()
+        return handle_holder._run(x, bias)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        input, weight, bias = ctx.saved_tensors
+        padding = ctx.padding
+        grad_input = grad_weight = grad_bias = None
+        go = grad_output.contiguous()
+        if ctx.needs_input_grad[0]:
+            grad_input = _grad_input(go, weight, padding, input.dtype)
+        if ctx.needs_input_grad[1]:
+            grad_weight = _grad_weight(input, go, weight, padding)
+        if bias is not None and ctx.needs_input_grad[2]:
+            grad_bias = go.float().sum(dim=(0, 2, 3)).to(bias.dtype)
+        return grad_input, grad_weight, grad_bias, None, None
+
+
+# ─────────────────────────────────────────────────────────────────────────
+# NovaWinogradConv2d -- inference module
+# ─────────────────────────────────────────────────────────────────────────
+
+class NovaWinogradConv2d(nn.Module):
+    """Drop-in replacement for nn.Conv2d using NOVA Winograd F(6,3)
+    (/root/reference/nova_winograd/conv2d.py:154-273).
+
+    Supports kernel_size=3, stride=1 only. Input must be float16. Weights are
+    stored in float32 and transformed on first use and whenever they change.
+
+    Args:
+        in_channels:  Number of input channels.
+        out_channels: Number of output channels.
+        kernel_size:  Must be 3.
+        padding:      Convolution padding (default 1).
+        bias:         Whether to include bias (default False).
+    """
+
+    def __init__(self, in_channels, out_channels, kernel_size=3, padding=1, bias=False):
+        super().__init__()
+        assert kernel_size == 3, "Only 3x3 kernels supported"
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.padding = padding
+
+        self.weight = nn.Parameter(torch.empty(out_channels, in_channels, 3, 3))
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_channels))
+        else:
+            self.register_parameter("bias", None)
+
+        self._handle = None
+        self._weight_version = -1
+        self._V_gemm = None
+        self._M_gemm = None
+        self._last_config = None
+        self._tiling = None
+
+    # -- caches -------------------------------------------------------------
+    def invalidate_weight_cache(self):
+        """Force the filter transform to be rebuilt on the next forward (use
+        after writing the weights through ``.data``, which PyTorch does not
+        version)."""
+        self._weight_version = -1
+        if self._handle is not None:
+            self._handle.key = None
+
+    def _apply(self, fn, *args, **kwargs):
+        out = super()._apply(fn, *args, **kwargs)
+        self.invalidate_weight_cache()
+        self._V_gemm = self._M_gemm = None
+        self._last_config = None
+        return out
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        super()._load_from_state_dict(*args, **kwargs)
+        self.invalidate_weight_cache()
+
+    def _ensure_handle(self):
+        """Create the handle and re-transform the filter if the weight changed."""
+        if self._handle is None:
+            self._handle = _Handle()
+        hd = self._handle
+        hd.set_stream(self.weight.device)
+        key = _weight_key(self.weight)
+        if key != hd.key:
+            hd.set_weights(self.weight)
+            hd.key = key
+            self._weight_version = self.weight._version
+            self._V_gemm = None
+            self._M_gemm = None
+            self._last_config = None
+
+    def _ensure_workspace(self, batch, H, W):
+        """Allocate the reference-sized workspace when the configuration
+        changes (/root/reference/nova_winograd/conv2d.py:205-220). Layers
+        served by the fused kernel need none."""
+        config = (batch, H, W, self.padding)
+        if self._last_config != config:
+            nh, nw, H_out, W_out = compute_tiling(H, W, self.padding)
+            BP = batch * nh * nw
+            lib = self._handle.lib
+            need = lib.nova_workspace_bytes(self._handle.h, batch, H, W, self.padding)
+            check("workspace_bytes")
+            device = self.weight.device
+            if need > 0:
+                self._V_gemm = torch.empty(64, self.in_channels, BP, dtype=torch.float16,
+                                           device=device)
+                self._M_gemm = torch.empty(64, self.out_channels, BP, dtype=torch.float16,
+                                           device=device)
+            else:
+                self._V_gemm = self._M_gemm = None
+            self._tiling = (nh, nw, H_out, W_out)
+            self._last_config = config
+        return self._tiling
+
+    # -- forward ------------------------------------------------------------
+    def _run(self, x, bias):
+        """Launch the HIP path on a contiguous fp16 input; returns fp16."""
+        require_gpu_tensor(x, "input")
+        B, C, H, W = x.shape
+        if C != self.in_channels:
+            raise ValueError(f"expected {self.in_channels} input channels, got {C}")
+        self._ensure_handle()
+        nh, nw, H_out, W_out = self._ensure_workspace(B, H, W)
+        hd = self._handle
+        hd.set_stream(x.device)
+        output = torch.empty(B, self.out_channels, H_out, W_out, dtype=torch.float16,
+                             device=x.device)
+        V, M = self._V_gemm, self._M_gemm
+        hd.lib.nova_forward_workspace(
+            hd.h, x.data_ptr(), output.data_ptr(),
+            V.data_ptr() if V is not None else None,
+            M.data_ptr() if M is not None else None,
+            B, H, W, self.padding, nh, nw,
+        )
+        check("forward")
+        if bias is not None:
+            output = output + bias.half().view(1, -1, 1, 1)
+        return output
+
+    def forward(self, x):
+        assert x.dtype == torch.float16, f"Input must be float16, got {x.dtype}"
+        assert x.is_contiguous(), "Input must be contiguous"
+        assert x.dim() == 4 and x.shape[1] == self.in_channels
+        return self._run(x, self.bias)
+
+    @classmethod
+    def from_conv2d(cls, conv):
+        """Create from an existing nn.Conv2d
+        (/root/reference/nova_winograd/conv2d.py:253-267)."""
+        assert conv.kernel_size == (3, 3), "Only 3x3 kernels supported"
+        assert conv.stride == (1, 1), "Only stride=1 supported"
+        assert not isinstance(conv.padding, str), "padding must be numeric"
+        assert conv.padding[0] == conv.padding[1], "Only symmetric padding supported"
+        nova_conv = cls(
+            conv.in_channels, conv.out_channels,
+            kernel_size=3, padding=conv.padding[0],
+            bias=conv.bias is not None,
+        )
+        nova_conv = nova_conv.to(conv.weight.device)
+        nova_conv.weight.data.copy_(conv.weight.data.float())
+        if conv.bias is not None:
+            nova_conv.bias.data.copy_(conv.bias.data.float())
+        nova_conv.invalidate_weight_cache()
+        return nova_conv
+
+    def extra_repr(self):
+        return (
+            f"in_channels={self.in_channels}, out_channels={self.out_channels}, "
+            f"kernel_size=3, padding={self.padding}, tile=F(6,3), points=NOVA"
+        )
+
+
+# ─────────────────────────────────────────────────────────────────────────
+# NovaWinogradConv2dTrainable (/root/reference/nova_winograd/conv2d.py:280-293)
+# ─────────────────────────────────────────────────────────────────────────
+
+class NovaWinogradConv2dTrainable(NovaWinogradConv2d):
+    """NOVA conv with backward support: HIP forward, fp32 backward."""
+
+    def forward(self, x):
+        if not x.is_contiguous():
+            x = x.contiguous()
+        if x.dtype != torch.float16:
+            x = x.half()
+        assert x.shape[1] == self.in_channels
+        return NovaWinogradFunction.apply(x, self.weight, self.bias, self.padding, self)
+
+
+# ─────────────────────────────────────────────────────────────────────────
+# NovaWinogradConv2dCompilable (/root/reference/nova_winograd/conv2d.py:300-344)
+# ─────────────────────────────────────────────────────────────────────────
+
+class NovaWinogradConv2dCompilable(nn.Module):
+    """NOVA conv compatible with torch.compile(fullgraph=True) through the
+    custom op ``torch.ops.nova.winograd_conv2d``."""
+
+    def __init__(self, in_channels, out_channels, kernel_size=3, padding=1, bias=False):
+        super().__init__()
+        assert kernel_size == 3
+        _register_custom_op()
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.padding = padding
+        self.weight = nn.Parameter(torch.empty(out_channels, in_channels, 3, 3))
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_channels))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x):
+        out = torch.ops.nova.winograd_conv2d(x, self.weight, self.padding)
+        if self.bias is not None:
+            out = out + self.bias.half().view(1, -1, 1, 1)
+        return out
+
+    @classmethod
+    def from_conv2d(cls, conv):
+        assert conv.kernel_size == (3, 3) and conv.stride == (1, 1)
+        assert not isinstance(conv.padding, str) and conv.padding[0] == conv.padding[1]
+        nova = cls(
+            conv.in_channels, conv.out_channels,
+            padding=conv.padding[0], bias=conv.bias is not None,
+        )
+        nova = nova.to(conv.weight.device)
+        nova.weight.data.copy_(conv.weight.data.float())
+        if conv.bias is not None:
+            nova.bias.data.copy_(conv.bias.data.float())
+        return nova
+
+    def extra_repr(self):
+        return (
+            f"in_channels={self.in_channels}, out_channels={self.out_channels}, "
+            f"kernel_size=3, padding={self.padding}, tile=F(6,3), points=NOVA, compilable=True"
+        )

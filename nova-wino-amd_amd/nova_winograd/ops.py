@@ -1,0 +1,186 @@
+"""ctypes bridge to libnova_winograd.so (the gfx950 HIP library).
+
+Mirrors the reference's bridge (/root/reference/nova_winograd/ops.py:1-176):
+same library name and search order, same functions (``get_lib``, ``ptr``,
+``compute_tiling``, ``nova_forward``) and the same C signatures. Differences:
+
+* loading the library does not initialise the GPU, so host-only entry points
+  (``compute_tiling``) work on a machine without one; every entry point that
+  touches device memory checks for a ROCm device and raises otherwise -- there
+  is no CPU fallback;
+* the library reports errors through ``nova_get_last_error`` instead of
+  exiting the process; :func:`check` turns them into ``RuntimeError``;
+* launches follow PyTorch's current stream (``nova_set_stream``).
+"""
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_lib = None
+_lib_lock = threading.Lock()
+_LIB_NAME = "libnova_winograd.so"
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_ip = ctypes.POINTER(ctypes.c_int)
+
+# name -> (restype, argtypes). The first twelve are the reference's
+# (/root/reference/nova_winograd/ops.py:66-114); the rest are this library's.
+_SIGNATURES = {
+    "nova_create": (_vp, []),
+    "nova_destroy": (None, [_vp]),
+    "nova_set_weights": (None, [_vp, _vp, _i, _i]),
+    "nova_forward": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "nova_forward_workspace": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i]),
+    "nova_compute_tiling": (None, [_i, _i, _i, _ip, _ip, _ip, _ip]),
+    "nova_filter_transform": (None, [_vp, _vp, _i, _i]),
+    "nova_input_transform": (None, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i]),
+    "nova_output_transform": (None, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
+    "nova_get_K": (_i, [_vp]),
+    "nova_get_C": (_i, [_vp]),
+    "nova_get_U_gemm": (_vp, [_vp]),
+    # reference fused C-API (/root/reference/csrc/nova_winograd_fused.hip:619-652)
+    "nova_fused_create": (_vp, []),
+    "nova_fused_destroy": (None, [_vp]),
+    "nova_fused_set_weights": (None, [_vp, _vp, _i, _i]),
+    "nova_fused_forward": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "nova_fused_compute_tiling": (None, [_i, _i, _i, _ip, _ip, _ip, _ip]),
+    # extensions
+    "nova_get_last_error": (_i, []),
+    "nova_get_last_error_message": (ctypes.c_char_p, []),
+    "nova_set_stream": (None, [_vp, _vp]),
+    "nova_set_path": (None, [_vp, _i]),
+    "nova_get_last_path": (_i, [_vp]),
+    "nova_workspace_bytes": (ctypes.c_longlong, [_vp, _i, _i, _i, _i]),
+    "nova_version": (ctypes.c_char_p, []),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def _find_lib():
+    """Locate the shared library: package ``lib/`` first, then the cwd
+    (same order as /root/reference/nova_winograd/ops.py:16-28)."""
+    candidates = [
+        os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", _LIB_NAME),
+        os.path.join(os.getcwd(), _LIB_NAME),
+    ]
+    for path in candidates:
+        if os.path.exists(path):
+            return path
+    raise FileNotFoundError(
+        f"Cannot find {_LIB_NAME}. Build it with: make -C nova-wino-amd_amd "
+        f"(or python -c 'import __graft_entry__ as g; g.build()')\nSearched: {candidates}"
+    )
+
+
+def _ensure_lib():
+    """Load the library once per process and declare every signature."""
+    global _lib
+    if _lib is not None:
+        return
+    with _lib_lock:
+        if _lib is not None:
+            return
+        lib = ctypes.CDLL(_find_lib(), mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+
+
+def get_lib():
+    """Get the loaded ctypes library handle."""
+    _ensure_lib()
+    return _lib
+
+
+def lib_path():
+    """Filesystem path of the loaded library."""
+    return _find_lib()
+
+
+def ptr(tensor):
+    """Raw device pointer of a tensor (as the reference's ``ptr``)."""
+    return ctypes.c_void_p(tensor.data_ptr())
+
+
+def check(where=""):
+    """Raise RuntimeError if the library recorded an error on this thread."""
+    lib = get_lib()
+    code = lib.nova_get_last_error()
+    if code:
+        msg = lib.nova_get_last_error_message().decode(errors="replace")
+        raise RuntimeError(f"nova_winograd{(' ' + where) if where else ''}: {msg} (code {code})")
+
+
+def require_gpu_tensor(t, name="input"):
+    """The product path runs only on a ROCm GPU; fail loudly otherwise."""
+    if not t.is_cuda:
+        raise RuntimeError(
+            f"nova_winograd: {name} is on {t.device}; NOVA Winograd runs only on a ROCm GPU "
+            "(no CPU fallback)"
+        )
+
+
+def current_stream_ptr(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def compute_tiling(H, W, pad):
+    """Tiling parameters (nh, nw, H_out, W_out) by the reference's law
+    (/root/reference/csrc/nova_winograd.hip:617-631): nh = ceil((Ho-1)/6)+1."""
+    _ensure_lib()
+    nh, nw, H_out, W_out = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _lib.nova_compute_tiling(
+        H, W, pad,
+        ctypes.byref(nh), ctypes.byref(nw), ctypes.byref(H_out), ctypes.byref(W_out),
+    )
+    return nh.value, nw.value, H_out.value, W_out.value
+
+
+def nova_forward(input_fp16, weight_fp32, padding=1):
+    """Functional API: NOVA Winograd F(6,3) forward pass
+    (/root/reference/nova_winograd/ops.py:147-176).
+
+    Args:
+        input_fp16:  [B, C, H, W] float16 tensor on GPU.
+        weight_fp32: [K, C, 3, 3] float32 tensor on GPU.
+        padding:     Convolution padding (default 1).
+
+    Returns:
+        output: [B, K, H_out, W_out] float16 tensor on GPU.
+
+    Like the reference it creates a handle, transforms the filter, runs and
+    destroys the handle; all work is ordered on PyTorch's current stream, so
+    no device-wide synchronisation is needed around it.
+    """
+    _ensure_lib()
+    require_gpu_tensor(input_fp16, "input")
+    require_gpu_tensor(weight_fp32, "weight")
+    assert input_fp16.dtype == torch.float16
+    assert weight_fp32.dtype == torch.float32
+    assert input_fp16.is_contiguous() and weight_fp32.is_contiguous()
+    assert input_fp16.dim() == 4 and weight_fp32.dim() == 4
+    assert tuple(weight_fp32.shape[1:]) == (input_fp16.shape[1], 3, 3)
+
+    B, C, H, W = input_fp16.shape
+    K = weight_fp32.shape[0]
+    nh, nw, H_out, W_out = compute_tiling(H, W, padding)
+    output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=input_fp16.device)
+
+    handle = _lib.nova_create()
+    try:
+        _lib.nova_set_stream(handle, current_stream_ptr(input_fp16.device))
+        _lib.nova_set_weights(handle, ptr(weight_fp32), K, C)
+        check("set_weights")
+        _lib.nova_forward(handle, ptr(input_fp16), ptr(output), B, H, W, padding)
+        check("forward")
+    finally:
+        # nova_destroy frees device memory; hipFree waits for queued work.
+        _lib.nova_destroy(handle)
+    return output

@@ -1,0 +1,262 @@
+"""Parity of the gfx950 HIP path with the CPU oracle, stage by stage and end
+to end, through the C-ABI.
+
+Bars:
+* filter, input and output transforms: bit-exact (same fp32 FMA chains and
+  fp16 rounding points as the oracle);
+* Winograd-domain GEMM: |M_gpu - M_oracle| <= 2*C*2^-24*sum|U||V| + 1 ulp16,
+  the fp32 summation bound for any accumulation order (the oracle's M is the
+  correctly rounded one);
+* whole path: rel-L2(gpu, oracle) <= 5e-3, max-abs <= 0.25 at unit-scale
+  outputs; against the fp64 direct convolution the GPU error is no worse than
+  1.05x the oracle's rel-L2 and 1.25x its max-abs; zero NaN/Inf.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _lib():
+    from nova_winograd.ops import get_lib
+
+    return get_lib()
+
+
+def _check():
+    from nova_winograd.ops import check
+
+    check()
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def assert_same_bits(got, want, what=""):
+    """Bit-exact comparison of two fp16 arrays with a compact report."""
+    g = np.ascontiguousarray(got).view(np.uint16)
+    w = np.ascontiguousarray(want).view(np.uint16)
+    assert g.shape == w.shape, (g.shape, w.shape)
+    bad = np.flatnonzero(g != w)
+    if bad.size:
+        first = bad[:6]
+        idx = [tuple(int(v) for v in t) for t in zip(*np.unravel_index(first, g.shape))]
+        gv = g.flat[first].view(np.float16).astype(np.float32)
+        wv = w.flat[first].view(np.float16).astype(np.float32)
+        raise AssertionError(
+            f"{what}: {bad.size}/{g.size} elements differ; first at {idx}: "
+            f"got {gv.tolist()} want {wv.tolist()} (bits {g.flat[first].tolist()} vs "
+            f"{w.flat[first].tolist()})")
+
+
+def _ulp16(x):
+    a = np.abs(x.astype(np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def _kaiming(K, C, gen=None):
+    w = torch.empty(K, C, 3, 3)
+    torch.nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu", generator=gen)
+    return w
+
+
+FILTER_CASES = [(64, 64), (48, 192), (8, 3), (128, 256), (40, 24), (1, 1)]
+
+
+@pytest.mark.parametrize("K,C", FILTER_CASES)
+def test_filter_transform_bitexact(oracle, K, C):
+    print(f"[filter] K={K} C={C}", flush=True)
+    w = torch.randn(K, C, 3, 3) * 0.7
+    U = torch.empty(64, C, K, dtype=torch.float16, device=DEV)
+    _lib().nova_filter_transform(w.to(DEV).data_ptr(), U.data_ptr(), K, C)
+    _check()
+    ref = oracle.filter_transform(w.numpy())
+    assert_same_bits(_u16(U), ref, f"U K={K} C={C}")
+
+
+INPUT_CASES = [
+    (1, 64, 56, 56, 1), (2, 3, 13, 13, 1), (1, 128, 28, 28, 1), (1, 16, 7, 7, 1),
+    (1, 24, 14, 9, 0), (1, 8, 11, 11, 2), (3, 72, 20, 17, 1), (1, 130, 5, 5, 1),
+]
+
+
+@pytest.mark.parametrize("B,C,H,W,pad", INPUT_CASES)
+def test_input_transform_bitexact(oracle, B, C, H, W, pad):
+    print(f"[input] B={B} C={C} H={H} W={W} pad={pad}", flush=True)
+    x = torch.randn(B, C, H, W).half()
+    nh, nw, Ho, Wo = oracle.tiling(H, W, pad)
+    BP = B * nh * nw
+    V = torch.full((64, BP, C), float("nan"), dtype=torch.float16, device=DEV)
+    _lib().nova_input_transform(x.to(DEV).data_ptr(), V.data_ptr(), B, C, H, W, pad, nh, nw, BP)
+    _check()
+    ref = oracle.input_transform(x.numpy(), pad, nh, nw)
+    assert_same_bits(_u16(V), ref, "V")
+
+
+OUTPUT_CASES = [(1, 64, 56, 56), (2, 48, 14, 14), (1, 130, 7, 9), (3, 8, 13, 11), (1, 16, 1, 1)]
+
+
+@pytest.mark.parametrize("B,K,Ho,Wo", OUTPUT_CASES)
+def test_output_transform_bitexact(oracle, B, K, Ho, Wo):
+    print(f"[output] B={B} K={K} Ho={Ho} Wo={Wo}", flush=True)
+    # reference tiling for pad=1 (H = Ho)
+    nh, nw, _, _ = oracle.tiling(Ho, Wo, 1)
+    BP = B * nh * nw
+    M = (torch.randn(64, BP, K) * 3).half()
+    y = torch.full((B, K, Ho, Wo), float("nan"), dtype=torch.float16, device=DEV)
+    _lib().nova_output_transform(M.to(DEV).data_ptr(), y.data_ptr(), B, K, Ho, Wo, nh, nw, BP)
+    _check()
+    ref = oracle.output_transform(M.numpy(), B, Ho, Wo, nh, nw)
+    assert_same_bits(_u16(y), ref, "y")
+
+
+GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256, 28),
+              (1, 256, 256, 14), (1, 16, 40, 9)]
+
+
+@pytest.mark.parametrize("B,C,K,H", GEMM_CASES)
+def test_gemm_within_fp32_bound(oracle, B, C, K, H):
+    """White-box: force the 3-pass path with caller workspaces; for C % 8 == 0
+    the workspace then holds V[64][BP][C] and M[64][BP][K] at the minimal
+    tiling ceil(Ho/6) x ceil(Wo/6)."""
+    print(f"[gemm] B={B} C={C} K={K} H={H}", flush=True)
+    assert C % 8 == 0
+    lib = _lib()
+    x = torch.randn(B, C, H, H).half()
+    w = _kaiming(K, C)
+    nh, nw, Ho, Wo = oracle.tiling(H, H, 1)
+    nhm, nwm = -(-Ho // 6), -(-Wo // 6)
+    BP, BPm = B * nh * nw, B * nhm * nwm
+    V = torch.empty(64 * C * BP, dtype=torch.float16, device=DEV)
+    M = torch.empty(64 * K * BP, dtype=torch.float16, device=DEV)
+    y = torch.empty(B, K, Ho, Wo, dtype=torch.float16, device=DEV)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_path(h, 1)
+        wd = w.to(DEV)
+        lib.nova_set_weights(h, wd.data_ptr(), K, C)
+        xd = x.to(DEV)
+        lib.nova_forward_workspace(h, xd.data_ptr(), y.data_ptr(), V.data_ptr(), M.data_ptr(),
+                                   B, H, H, 1, nh, nw)
+        _check()
+        assert lib.nova_get_last_path(h) == 1
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    Vg = V[: 64 * C * BPm].view(64, BPm, C)
+    Mg = M[: 64 * K * BPm].view(64, BPm, K)
+    Vo = oracle.input_transform(x.numpy(), 1, nhm, nwm)
+    assert_same_bits(_u16(Vg), Vo, "V (workspace)")
+    Uo = oracle.filter_transform(w.numpy())
+    Mo, Mabs = oracle.batched_gemm(Uo, Vo, with_abs=True)
+    mg = Mg.float().cpu().numpy().astype(np.float64)
+    mo = Mo.astype(np.float64)
+    bound = 2.0 * C * 2.0 ** -24 * Mabs.astype(np.float64) + _ulp16(mo) * 1.0001
+    err = np.abs(mg - mo)
+    assert np.isfinite(mg).all()
+    worst = np.argmax(err - bound)
+    assert (err <= bound).all(), f"M mismatch at {np.unravel_index(worst, err.shape)}: err {err.flat[worst]} bound {bound.flat[worst]}"
+    # the output transform of the GPU's own M is bit-exact
+    yo = oracle.output_transform(Mg.cpu().numpy(), B, Ho, Wo, nhm, nwm)
+    assert_same_bits(_u16(y), yo, "y from GPU M")
+
+
+FORWARD_CASES = [
+    # (B, C, K, H, W, pad) -- BASELINE configs 1-2 and edge shapes
+    (1, 64, 64, 56, 56, 1),
+    (1, 128, 128, 28, 28, 1),
+    (1, 256, 256, 14, 14, 1),
+    (1, 512, 512, 7, 7, 1),
+    (1, 192, 48, 56, 56, 1),
+    (1, 192, 48, 7, 7, 1),
+    (2, 3, 64, 32, 32, 1),
+    (2, 20, 36, 13, 17, 0),
+    (1, 40, 24, 10, 10, 2),
+]
+
+
+def _forward_case(oracle, B, C, K, H, W, pad, path):
+    torch.manual_seed(0)
+    x = torch.randn(B, C, H, W).half()
+    w = _kaiming(K, C)
+    lib = _lib()
+    h = lib.nova_create()
+    Ho, Wo = H + 2 * pad - 2, W + 2 * pad - 2
+    y = torch.empty(B, K, Ho, Wo, dtype=torch.float16, device=DEV)
+    try:
+        lib.nova_set_path(h, path)
+        wd, xd = w.to(DEV), x.to(DEV)
+        lib.nova_set_weights(h, wd.data_ptr(), K, C)
+        lib.nova_forward(h, xd.data_ptr(), y.data_ptr(), B, H, W, pad)
+        _check()
+        took = lib.nova_get_last_path(h)
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    yg = y.cpu().numpy()
+    yo = oracle.conv2d(x.numpy(), w.numpy(), pad)
+    truth = oracle.direct_conv2d(x.numpy(), w.numpy(), pad)
+    return yg, yo, truth, took
+
+
+@pytest.mark.parametrize("B,C,K,H,W,pad", FORWARD_CASES)
+def test_forward_matches_oracle(oracle, B, C, K, H, W, pad):
+    print(f"[forward] B={B} C={C} K={K} H={H} W={W} pad={pad}", flush=True)
+    yg, yo, truth, _ = _forward_case(oracle, B, C, K, H, W, pad, 0)
+    assert np.isfinite(yg.astype(np.float32)).all()
+    rel = oracle.rel_l2(yg, yo)
+    assert rel <= 5e-3, rel
+    assert oracle.max_abs(yg, yo) <= 0.25
+    rel_g, rel_o = oracle.rel_l2(yg, truth), oracle.rel_l2(yo, truth)
+    mx_g, mx_o = oracle.max_abs(yg, truth), oracle.max_abs(yo, truth)
+    assert rel_g <= 1.05 * rel_o, (rel_g, rel_o)
+    assert mx_g <= 1.25 * mx_o, (mx_g, mx_o)
+
+
+def test_forward_deterministic():
+    lib = _lib()
+    x = torch.randn(2, 64, 28, 28, device=DEV).half()
+    w = _kaiming(64, 64).to(DEV)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_weights(h, w.data_ptr(), 64, 64)
+        outs = []
+        for _ in range(3):
+            y = torch.empty(2, 64, 28, 28, dtype=torch.float16, device=DEV)
+            lib.nova_forward(h, x.data_ptr(), y.data_ptr(), 2, 28, 28, 1)
+            _check()
+            outs.append(y.clone())
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_forward_follows_stream(oracle):
+    """Work goes to the stream set on the handle, ordered after the producer
+    of its input on that stream."""
+    lib = _lib()
+    s = torch.cuda.Stream()
+    w = _kaiming(32, 32).to(DEV)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_stream(h, ctypes.c_void_p(s.cuda_stream))
+        with torch.cuda.stream(s):
+            x = torch.randn(1, 32, 20, 20, device=DEV).half()
+            lib.nova_set_weights(h, w.data_ptr(), 32, 32)
+            y = torch.empty(1, 32, 20, 20, dtype=torch.float16, device=DEV)
+            lib.nova_forward(h, x.data_ptr(), y.data_ptr(), 1, 20, 20, 1)
+            _check()
+        s.synchronize()
+        yo = oracle.conv2d(x.cpu().numpy(), w.cpu().numpy(), 1)
+    finally:
+        lib.nova_destroy(h)
+    assert oracle.rel_l2(y.cpu().numpy(), yo) < 5e-3

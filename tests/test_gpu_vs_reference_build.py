@@ -1,0 +1,147 @@
+"""Cross-check against the reference's own library, compiled from its source
+by oracle/Makefile (`make -C oracle ref` -> oracle/_ref/libnova_winograd_ref.so,
+built with hipcc for gfx950 and linked to the image's rocBLAS).
+
+This pins the CPU oracle (and through it this build) to what the reference
+actually computes on the same inputs. The reference's own kernels are not
+bit-consistent with each other (its forward input transform compiles to
+separate multiply+add, its output transform to fused multiply-adds, and the
+rocBLAS accumulation order is unspecified), so the bars are:
+  * input/output/filter transforms: identical fp16 bits except for rare
+    1-ulp differences (fraction of differing elements < 1e-2, none > 1 ulp);
+  * whole path (rocBLAS GEMM inside): rel-L2 to this build <= 5e-3 and both
+    at the same error level against the fp64 direct convolution.
+Skipped when the reference library was not built (no reference tree).
+"""
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+REF_SO = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle",
+                      "_ref", "libnova_winograd_ref.so")
+
+_ref = None
+
+
+def ref_lib():
+    global _ref
+    if _ref is None:
+        if not os.path.exists(REF_SO):
+            pytest.skip("reference library not built (oracle/_ref)")
+        torch.cuda.init()
+        L = ctypes.CDLL(REF_SO, mode=ctypes.RTLD_LOCAL)
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        L.nova_create.restype = vp
+        L.nova_create.argtypes = []
+        L.nova_destroy.argtypes = [vp]
+        L.nova_set_weights.argtypes = [vp, vp, i, i]
+        L.nova_forward.argtypes = [vp, vp, vp, i, i, i, i]
+        L.nova_filter_transform.argtypes = [vp, vp, i, i]
+        L.nova_input_transform.argtypes = [vp, vp] + [i] * 8
+        L.nova_output_transform.argtypes = [vp, vp] + [i] * 7
+        _ref = L
+    return _ref
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _ulp_distance(a, b):
+    """Distance in fp16 ulps between two same-sign-or-zero fp16 bit arrays."""
+    a = a.astype(np.int32)
+    b = b.astype(np.int32)
+    sa = np.where(a & 0x8000, -(a & 0x7FFF), a & 0x7FFF)
+    sb = np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    return np.abs(sa - sb)
+
+
+def _near_bitexact(got, want, what):
+    d = _ulp_distance(got, want)
+    frac = float((d > 0).mean())
+    print(f"{what}: {int((d > 0).sum())}/{d.size} differ (max {int(d.max())} ulp)", flush=True)
+    assert d.max() <= 1, f"{what}: max ulp distance {d.max()}"
+    assert frac < 1e-2, f"{what}: {frac:.3%} of elements differ"
+
+
+def test_reference_filter_transform():
+    L = ref_lib()
+    K, C = 64, 96
+    w = (torch.randn(K, C, 3, 3) * 0.5).to(DEV)
+    U_ref = torch.empty(64, C, K, dtype=torch.float16, device=DEV)
+    L.nova_filter_transform(w.data_ptr(), U_ref.data_ptr(), K, C)
+    torch.cuda.synchronize()
+    from nova_winograd.ops import check, get_lib
+
+    U = torch.empty_like(U_ref)
+    get_lib().nova_filter_transform(w.data_ptr(), U.data_ptr(), K, C)
+    check()
+    _near_bitexact(_u16(U), _u16(U_ref), "U")
+
+
+@pytest.mark.parametrize("B,C,H,pad", [(1, 64, 56, 1), (2, 24, 13, 0), (1, 40, 9, 2)])
+def test_reference_input_transform(oracle, B, C, H, pad):
+    L = ref_lib()
+    x = torch.randn(B, C, H, H).half()
+    nh, nw, _, _ = oracle.tiling(H, H, pad)
+    BP = B * nh * nw
+    V_ref = torch.empty(64, BP, C, dtype=torch.float16, device=DEV)
+    L.nova_input_transform(x.to(DEV).data_ptr(), V_ref.data_ptr(), B, C, H, H, pad, nh, nw, BP)
+    torch.cuda.synchronize()
+    Vo = oracle.input_transform(x.numpy(), pad, nh, nw)
+    _near_bitexact(Vo.view(np.uint16), _u16(V_ref), "V oracle vs reference")
+
+
+@pytest.mark.parametrize("B,K,Ho", [(1, 64, 56), (2, 48, 14)])
+def test_reference_output_transform(oracle, B, K, Ho):
+    L = ref_lib()
+    nh, nw, _, _ = oracle.tiling(Ho, Ho, 1)
+    BP = B * nh * nw
+    M = (torch.randn(64, BP, K) * 3).half()
+    y_ref = torch.zeros(B, K, Ho, Ho, dtype=torch.float16, device=DEV)
+    L.nova_output_transform(M.to(DEV).data_ptr(), y_ref.data_ptr(), B, K, Ho, Ho, nh, nw, BP)
+    torch.cuda.synchronize()
+    yo = oracle.output_transform(M.numpy(), B, Ho, Ho, nh, nw)
+    _near_bitexact(yo.view(np.uint16), _u16(y_ref), "y oracle vs reference")
+
+
+@pytest.mark.parametrize("B,C,K,H", [(1, 64, 64, 56), (1, 128, 128, 28), (1, 256, 256, 14),
+                                     (1, 512, 512, 7), (2, 192, 48, 14)])
+def test_reference_whole_path(oracle, B, C, K, H):
+    print(f"[ref path] B={B} C={C} K={K} H={H}", flush=True)
+    L = ref_lib()
+    torch.manual_seed(0)
+    x = torch.randn(B, C, H, H).half()
+    w = torch.empty(K, C, 3, 3)
+    torch.nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu")
+    xd, wd = x.to(DEV), w.to(DEV)
+    y_ref = torch.empty(B, K, H, H, dtype=torch.float16, device=DEV)
+    h = L.nova_create()
+    L.nova_set_weights(h, wd.data_ptr(), K, C)
+    torch.cuda.synchronize()
+    L.nova_forward(h, xd.data_ptr(), y_ref.data_ptr(), B, H, H, 1)
+    torch.cuda.synchronize()
+    L.nova_destroy(h)
+    import nova_winograd as nw
+
+    y = nw.nova_forward(xd, wd.contiguous(), 1)
+    torch.cuda.synchronize()
+    truth = oracle.direct_conv2d(x.numpy(), w.numpy(), 1)
+    yr, yg = y_ref.cpu().numpy(), y.cpu().numpy()
+    yo = oracle.conv2d(x.numpy(), w.numpy(), 1)
+    rel_ref, rel_gpu, rel_or = (oracle.rel_l2(a, truth) for a in (yr, yg, yo))
+    print(f"rel-L2 vs fp64: reference {rel_ref:.4e}  this build {rel_gpu:.4e}  oracle {rel_or:.4e}; "
+          f"build vs reference {oracle.rel_l2(yg, yr):.2e}; oracle vs reference "
+          f"{oracle.rel_l2(yo, yr):.2e}", flush=True)
+    assert np.isfinite(yr.astype(np.float32)).all()
+    assert oracle.rel_l2(yg, yr) <= 5e-3
+    assert oracle.rel_l2(yo, yr) <= 5e-3
+    assert rel_gpu <= 1.05 * rel_ref
+    assert oracle.max_abs(yg, truth) <= 1.25 * oracle.max_abs(yr, truth)
