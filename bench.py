@@ -1,0 +1,398 @@
+#!/usr/bin/env python3
+"""Benchmark: NOVA F(6,3) Winograd 3x3 stride-1 convolution on one MI355X.
+
+Workload (BASELINE.json metric: per-layer ms + effective TFLOP/s on the
+ResNet-50 3x3 s1 convolutions at B=1 and B=32): the four layers
+conv2_x (64ch, 56^2), conv3_x (128, 28^2), conv4_x (256, 14^2),
+conv5_x (512, 7^2), pad 1, C=K, at B=1 and at B=32 -- eight layer runs.
+A "step" is one forward of all eight through the drop-in module
+(NovaWinogradConv2d), inputs resident in HBM, weights transformed once.
+
+Reported on one JSON line (stdout):
+  value        effective TFLOP/s of the step = sum of direct-conv FLOPs
+               (2*B*K*C*Ho*Wo*9, /root/reference/benchmarks/bench_layers.py:58)
+               / step time
+  layers       per layer: NOVA ms and MIOpen (nn.Conv2d fp16) ms, eager and
+               HIP-graph replayed, effective TFLOP/s, path, roofline fraction
+               T_roof/T (T_roof = max(2*64*K*C*B*P_min / 2.5 PF,
+               (2BCHW + 2BKHoWo + 2*64*K*C) / 8 TB/s))
+  roofline     the dominant kernel of the step (largest summed time), timed
+               live with the library's hipEvents on its launch stream:
+               algorithmic bytes per launch / average launch time vs 8 TB/s
+  cpu_baseline the CPU oracle (the reference's NOVA arithmetic, C, OpenMP) on
+               a bounded sample of the same layers, on this host's cores
+
+Synthetic inputs: torch.manual_seed(0) per layer, x ~ N(0,1) fp16,
+w Kaiming-normal (fan_in, relu) fp32, no bias.
+"""
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "nova-wino-amd_amd")
+for _p in (PKG_DIR, ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "per-layer ms + effective TFLOP/s, ResNet-50 3x3 s1 convs at B=1 and B=32"
+LAYERS = [("conv2_x", 64, 56), ("conv3_x", 128, 28), ("conv4_x", 256, 14), ("conv5_x", 512, 7)]
+BATCHES = [1, 32]
+PEAK_HBM_GBS = 8000.0
+PEAK_FP16_TFLOPS = 2500.0
+KIND_NAMES = ["input", "gemm", "output", "fused"]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def direct_flops(B, C, K, Ho, Wo):
+    return 2.0 * B * K * C * Ho * Wo * 9
+
+
+def layer_roofline_us(B, C, K, H):
+    Ho = Wo = H
+    pmin = -(-Ho // 6) * -(-Wo // 6)
+    f_alg = 2.0 * 64 * K * C * B * pmin
+    b_alg = 2.0 * B * C * H * H + 2.0 * B * K * Ho * Wo + 2.0 * 64 * K * C
+    return max(f_alg / (PEAK_FP16_TFLOPS * 1e12), b_alg / (PEAK_HBM_GBS * 1e9)) * 1e6
+
+
+def kernel_alg_bytes(kind, B, C, K, H):
+    """Algorithmic HBM bytes of one launch of a kernel kind (fp16 = 2 B):
+    input transform reads x, writes V; GEMM reads U and V, writes M; output
+    transform reads M, writes y; fused reads x and U, writes y. Minimal
+    tiling P = ceil(Ho/6)^2, channel pitch C rounded up to 8."""
+    Cp = (C + 7) // 8 * 8
+    Ho = H
+    BP = B * (-(-Ho // 6)) ** 2
+    x, y = 2 * B * C * H * H, 2 * B * K * Ho * Ho
+    V, M, U = 2 * 64 * Cp * BP, 2 * 64 * K * BP, 2 * 64 * K * Cp
+    return {"input": x + V, "gemm": U + V + M, "output": M + y, "fused": x + U + y}[kind]
+
+
+def time_region(fn, reps, torch):
+    """Mean ms per call over `reps` calls, CUDA events on the current stream."""
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def graph_of(fn, torch):
+    """Capture fn into a HIP graph (after an eager warm-up); None if capture
+    is not possible."""
+    try:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        torch.cuda.synchronize()
+        return g
+    except Exception as exc:  # report, do not hide: the field becomes null
+        log(f"graph capture failed: {exc!r}")
+        torch.cuda.synchronize()
+        return None
+
+
+def load_traffic(kernel_name, layer_desc):
+    """HBM bytes per launch measured offline with rocprofv3 FETCH_SIZE /
+    WRITE_SIZE (profiles/traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    for rec in data.get("kernels", []):
+        if rec.get("kernel") == kernel_name and rec.get("workload") == layer_desc:
+            return rec.get("hbm_bytes_per_launch")
+    return None
+
+
+def cpu_baseline(layers_spec, budget_s, threads):
+    """Time the CPU oracle (C restatement of the reference arithmetic, OpenMP)
+    on a bounded sample: every B=1 layer, and each B=32 layer on `sample_b`
+    images (work and FLOPs scale linearly in B)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    O.set_threads(threads)
+    torch.set_num_threads(threads)
+    sample_b = 2
+    jobs = []
+    for (name, C, H), B in layers_spec:
+        b = B if B == 1 else sample_b
+        torch.manual_seed(0)
+        x = torch.randn(b, C, H, H).half().numpy()
+        w = torch.empty(C, C, 3, 3)
+        torch.nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu")
+        jobs.append((name, B, b, x, w.numpy()))
+    flops = 0.0
+    secs = 0.0
+    conv_secs = 0.0
+    conv_flops = 0.0
+    rounds = 0
+    t_start = time.perf_counter()
+    while rounds == 0 or (time.perf_counter() - t_start) < budget_s:
+        for name, B, b, x, w in jobs:
+            t0 = time.perf_counter()
+            O.conv2d(x, w, 1)
+            secs += time.perf_counter() - t0
+            flops += direct_flops(b, x.shape[1], w.shape[0], x.shape[2], x.shape[3])
+        rounds += 1
+        if rounds >= 50:
+            break
+    # F.conv2d fp32 on the same sample, once per job (reference CPU path (b))
+    import torch.nn.functional as F
+
+    with torch.no_grad():
+        for name, B, b, x, w in jobs:
+            xt, wt = torch.from_numpy(x.astype(np.float32)), torch.from_numpy(w)
+            F.conv2d(xt, wt, padding=1)
+            t0 = time.perf_counter()
+            F.conv2d(xt, wt, padding=1)
+            conv_secs += time.perf_counter() - t0
+            conv_flops += direct_flops(b, x.shape[1], w.shape[0], x.shape[2], x.shape[3])
+    return {
+        "value": flops / secs / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle NOVA F(6,3) path (C, OpenMP {threads} threads) over the 4 ResNet-50 "
+                   f"layers at B=1 and on {sample_b} of the 32 images per B=32 layer, "
+                   f"{rounds} round(s), {secs:.1f} s; effective TFLOP/s with the direct-conv "
+                   "FLOP count"),
+        "ms_per_step_equiv": 1e3 * secs / rounds * (
+            sum(direct_flops(B, C, C, H, H) for (n, C, H), B in layers_spec)
+            / (flops / rounds)),
+        "fconv2d_fp32_tflops": conv_flops / conv_secs / 1e12,
+        "host": platform.processor() or platform.machine(),
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layer-reps", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-miopen", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--details", default="", help="write the full per-layer report here")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the NOVA conv shards by batch or output channel with no exchange; "
+              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import torch.nn as nn
+
+    import nova_winograd as nw
+    from nova_winograd.ops import get_lib
+
+    lib = get_lib()
+    dev = torch.device("cuda:0")
+    prop = torch.cuda.get_device_properties(dev)
+    log(f"device: {prop.name} ({getattr(prop, 'gcnArchName', '?')}), "
+        f"{prop.multi_processor_count} CUs, lib {lib.nova_version().decode()}")
+
+    spec = [(layer, B) for B in BATCHES for layer in LAYERS]
+    runs = []
+    for (name, C, H), B in spec:
+        torch.manual_seed(0)
+        x = torch.randn(B, C, H, H).half().to(dev)
+        w = torch.empty(C, C, 3, 3)
+        nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu")
+        mod = nw.NovaWinogradConv2d(C, C, kernel_size=3, padding=1).to(dev)
+        with torch.no_grad():
+            mod.weight.copy_(w.to(dev))
+        mio = nn.Conv2d(C, C, 3, padding=1, bias=False).to(dev).half()
+        with torch.no_grad():
+            mio.weight.copy_(w.half().to(dev))
+        runs.append({"name": name, "B": B, "C": C, "K": C, "H": H, "x": x, "mod": mod,
+                     "mio": mio})
+
+    total_flops = sum(direct_flops(r["B"], r["C"], r["K"], r["H"], r["H"]) for r in runs)
+
+    def step():
+        for r in runs:
+            r["mod"](r["x"])
+
+    with torch.no_grad():
+        # warm-up (filter transforms, workspaces, MIOpen solution search)
+        for _ in range(args.warmup):
+            step()
+        for r in runs:
+            r["mio"](r["x"])
+        torch.cuda.synchronize()
+
+        # ---- timed region: exactly K steps -----------------------------------
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ms_per_step = (t1 - t0) * 1e3 / args.steps
+        value = total_flops / (ms_per_step * 1e-3) / 1e12
+
+        # ---- per-kernel timing over a second K-step region ----------------------
+        for r in runs:
+            lib.nova_profile_enable(r["mod"]._handle.h, 1)
+        for _ in range(args.steps):
+            step()
+        import ctypes
+
+        kernels = {}
+        for r in runs:
+            tot = (ctypes.c_double * 4)()
+            cnt = (ctypes.c_longlong * 4)()
+            h = r["mod"]._handle.h
+            lib.nova_profile_read(h, tot, cnt)
+            r["kernels"] = {}
+            for k in range(4):
+                if cnt[k] == 0:
+                    continue
+                kname = lib.nova_profile_kernel_name(h, k).decode()
+                per = tot[k] / cnt[k]
+                ab = kernel_alg_bytes(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"])
+                r["kernels"][KIND_NAMES[k]] = {"kernel": kname, "avg_us": per * 1e3,
+                                              "alg_bytes": ab,
+                                              "gbs": ab / (per * 1e-3) / 1e9}
+                agg = kernels.setdefault(kname, {"ms": 0.0, "launches": 0, "bytes": 0.0,
+                                                 "by_layer": []})
+                agg["ms"] += tot[k]
+                agg["launches"] += cnt[k]
+                agg["bytes"] += ab * cnt[k]
+                agg["by_layer"].append(f"{r['name']}_b{r['B']}")
+            lib.nova_profile_enable(h, 0)
+
+        # ---- per-layer timings: NOVA vs MIOpen, eager and graph -----------------
+        for r in runs:
+            mod, mio, x = r["mod"], r["mio"], r["x"]
+            r["nova_ms"] = time_region(lambda: mod(x), args.layer_reps, torch)
+            r["path"] = {1: "3-pass", 2: "fused"}.get(lib.nova_get_last_path(mod._handle.h), "?")
+            if not args.no_miopen:
+                r["miopen_ms"] = time_region(lambda: mio(x), args.layer_reps, torch)
+            if not args.no_graph:
+                g = graph_of(lambda: mod(x), torch)
+                r["nova_graph_ms"] = (time_region(g.replay, args.layer_reps, torch)
+                                      if g is not None else None)
+                if not args.no_miopen:
+                    gm = graph_of(lambda: mio(x), torch)
+                    r["miopen_graph_ms"] = (time_region(gm.replay, args.layer_reps, torch)
+                                            if gm is not None else None)
+
+    # ---- dominant kernel roofline -----------------------------------------------
+    dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms"])
+    avg_s = dom["ms"] / dom["launches"] * 1e-3
+    bytes_per_launch = dom["bytes"] / dom["launches"]
+    achieved = bytes_per_launch / avg_s / 1e9
+    dom_desc = ",".join(sorted(set(dom["by_layer"])))
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "traffic": load_traffic(dom_name, dom_desc),
+        "kernel": dom_name,
+        "avg_launch_us": round(avg_s * 1e6, 3),
+        "alg_bytes_per_launch": round(bytes_per_launch),
+        "launches_per_step": dom["launches"] // args.steps,
+        "share_of_kernel_time": round(dom["ms"] / sum(v["ms"] for v in kernels.values()), 3),
+        "layers": dom_desc,
+    }
+
+    layers_out = []
+    for r in runs:
+        f = direct_flops(r["B"], r["C"], r["K"], r["H"], r["H"])
+        troof = layer_roofline_us(r["B"], r["C"], r["K"], r["H"])
+        rec = {
+            "layer": r["name"], "B": r["B"], "C": r["C"], "K": r["K"], "H": r["H"],
+            "path": r["path"],
+            "nova_ms": round(r["nova_ms"], 5),
+            "nova_tflops": round(f / (r["nova_ms"] * 1e-3) / 1e12, 2),
+            "roofline_us": round(troof, 3),
+            "roofline_frac": round(troof / (r["nova_ms"] * 1e3), 4),
+            "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
+                            for kk, vv in v.items()} for k, v in r["kernels"].items()},
+        }
+        if "miopen_ms" in r:
+            rec["miopen_ms"] = round(r["miopen_ms"], 5)
+            rec["speedup_vs_miopen"] = round(r["miopen_ms"] / r["nova_ms"], 3)
+        if r.get("nova_graph_ms") is not None:
+            rec["nova_graph_ms"] = round(r["nova_graph_ms"], 5)
+        if r.get("miopen_graph_ms") is not None:
+            rec["miopen_graph_ms"] = round(r["miopen_graph_ms"], 5)
+        layers_out.append(rec)
+        log(f"{r['name']:8s} B={r['B']:<3d} {r['path']:6s} nova {r['nova_ms']*1e3:8.2f} us"
+            + (f"  miopen {r['miopen_ms']*1e3:8.2f} us" if "miopen_ms" in r else "")
+            + (f"  graph nova {r['nova_graph_ms']*1e3:7.2f} us" if r.get("nova_graph_ms") else "")
+            + (f" miopen {r['miopen_graph_ms']*1e3:7.2f} us" if r.get("miopen_graph_ms") else "")
+            + f"  roofline {troof:6.2f} us")
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline([(( r["name"], r["C"], r["H"]), r["B"]) for r in runs],
+                           args.cpu_seconds, threads)
+        cpu = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "resnet50_3x3s1_layers_b1_b32",
+            "layers": [f"{n}:C=K={C},H=W={H}" for n, C, H in LAYERS],
+            "batches": BATCHES,
+            "pad": 1,
+            "direct_gflop_per_step": round(total_flops / 1e9, 3),
+            "interface": "NovaWinogradConv2d module (ctypes C-ABI), eager",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "layers": layers_out,
+    }
+    if args.details:
+        with open(args.details, "w") as f:
+            json.dump({"bench": out, "kernels": kernels}, f, indent=2)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

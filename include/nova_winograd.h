@@ -120,6 +120,16 @@ NOVA_API int nova_get_last_path(nova_handle_t h);
 /* Internal workspace bytes a forward of this shape needs on this handle. */
 NOVA_API long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad);
 
+/* Per-kernel timing for measurement. enable != 0 records hipEvents on the
+ * handle's stream around each kernel of every forward (at most 4096 forwards
+ * between reads); nova_profile_read() waits for them, writes the total ms and
+ * launch count per kernel kind (0 input transform, 1 GEMM, 2 output
+ * transform, 3 fused) and resets. Returns the number of timed launches. */
+NOVA_API void nova_profile_enable(nova_handle_t h, int enable);
+NOVA_API int nova_profile_read(nova_handle_t h, double* total_ms, long long* count);
+/* Name of the kernel last timed for a kind (e.g. "wgemm_kernel<2, 2, 2, 2>"). */
+NOVA_API const char* nova_profile_kernel_name(nova_handle_t h, int kind);
+
 /* Library version string. */
 NOVA_API const char* nova_version(void);
 

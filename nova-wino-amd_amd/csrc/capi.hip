@@ -9,7 +9,9 @@
 // the process.
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
+#include <vector>
 
 #include "../../include/nova_winograd.h"
 #include "nova_internal.h"
@@ -31,6 +33,35 @@ namespace {
 
 constexpr uint32_t kMagic = 0x4e4f5641u;  // "NOVA"
 
+// Kernel kinds for per-kernel timing.
+enum Kind { kKindInput = 0, kKindGemm = 1, kKindOutput = 2, kKindFused = 3, kNumKinds = 4 };
+
+// Optional per-kernel timing: hipEvents recorded on the handle's stream
+// around every kernel a forward launches. Off by default (zero overhead).
+struct Profiler {
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    size_t next = 0;
+    struct Span {
+        int kind;
+        size_t e0, e1;
+    };
+    std::vector<Span> spans;
+    const char* names[kNumKinds] = {"", "", "", ""};
+
+    // Returns the index of a recorded event, or SIZE_MAX when disabled/exhausted.
+    size_t mark(hipStream_t s) {
+        if (!on || next >= pool.size()) return SIZE_MAX;
+        if (hipEventRecord(pool[next], s) != hipSuccess) return SIZE_MAX;
+        return next++;
+    }
+    void span(int kind, size_t e0, size_t e1, const char* name) {
+        if (e0 == SIZE_MAX || e1 == SIZE_MAX) return;
+        spans.push_back({kind, e0, e1});
+        names[kind] = name;
+    }
+};
+
 struct Handle {
     uint32_t magic = kMagic;
     int K = 0, C = 0, Cp = 0;
@@ -42,6 +73,7 @@ struct Handle {
     int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused
     int last_path = 0;
     bool ready = false;
+    Profiler prof;
 };
 
 Handle* as_handle(nova_handle_t h, const char* fn) {
@@ -113,26 +145,64 @@ bool make_shape(const Handle* Hd, int B, int H, int W, int pad, Shape* s, const 
     s->nw = tiles_min(s->Wo);
     s->BP = (int64_t)B * s->nh * s->nw;
     const int cblocks = (Hd->Cp + 63) / 64, kblocks = (Hd->K + 63) / 64;
-    if (s->nh > 65535 || (int64_t)B * cblocks > 65535 || (int64_t)B * kblocks > 65535 ||
-        s->BP > (int64_t)1 << 30) {
+    if (s->nh > 65535 || (int64_t)B * cblocks > 65535 || (int64_t)B * kblocks > 65535) {
         set_error(kErrInvalidArgument, "%s: shape exceeds launch limits", fn);
         return false;
     }
     return true;
 }
 
+// Largest number of images per launch such that every buffer a kernel
+// addresses (x, y, V, M) stays below 2 GB: the kernels use 32-bit byte
+// offsets through buffer resources.
+int64_t batch_chunk(const Handle* Hd, const Shape& s) {
+    const int64_t P = (int64_t)s.nh * s.nw;
+    const int64_t per_img = std::max(
+        std::max(2 * (int64_t)Hd->C * s.H * s.W, 2 * (int64_t)Hd->K * s.Ho * s.Wo),
+        2 * 64 * (int64_t)std::max(Hd->Cp, Hd->K) * P);
+    return ((int64_t)1 << 31) / 2 / per_img;  // keep a 2x margin under INT_MAX
+}
+
 bool use_fused(const Handle* Hd, const Shape& s) {
     if (!fused_supported(Hd->K, Hd->C)) return false;
+    // per launch the batch is split so that x and y stay below 1 GB
+    const int64_t Bc = std::min<int64_t>(s.B, std::max<int64_t>(1, batch_chunk(Hd, s)));
+    if (!fused_fits(Bc * Hd->C * s.H * s.W, (int64_t)64 * Hd->K * Hd->Cp,
+                    Bc * Hd->K * s.Ho * s.Wo))
+        return false;
     if (Hd->path_pref == 2) return true;
     if (Hd->path_pref == 1) return false;
     // Automatic choice: the fused kernel wins when V/M round trips through
     // memory dominate, i.e. for small channel counts.
     return Hd->K <= 64 && Hd->C <= 64;
-    (void)s;
+}
+
+// Core forward on one sub-batch. V/M are workspaces large enough for it.
+bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* V,
+                    uint16_t* M) {
+    Profiler& pf = Hd->prof;
+    const size_t e0 = pf.mark(Hd->stream);
+    if (!hip_ok(launch_input_transform(x, V, s.B, Hd->C, s.H, s.W, s.pad, s.nh, s.nw, Hd->Cp,
+                                       (int64_t)Hd->Cp * s.BP, Hd->stream),
+                "input transform"))
+        return false;
+    const size_t e1 = pf.mark(Hd->stream);
+    if (!hip_ok(launch_wgemm(Hd->U, V, M, Hd->K, Hd->Cp, (int)s.BP, Hd->stream), "wgemm"))
+        return false;
+    const size_t e2 = pf.mark(Hd->stream);
+    if (!hip_ok(launch_output_transform(M, y, s.B, Hd->K, s.Ho, s.Wo, s.nh, s.nw, Hd->K,
+                                        (int64_t)Hd->K * s.BP, Hd->stream),
+                "output transform"))
+        return false;
+    const size_t e3 = pf.mark(Hd->stream);
+    pf.span(kKindInput, e0, e1, "input_transform_kernel");
+    pf.span(kKindGemm, e1, e2, wgemm_name(Hd->K, Hd->Cp, (int)s.BP));
+    pf.span(kKindOutput, e2, e3, "output_transform_kernel");
+    return true;
 }
 
 // Core forward. V_user/M_user may be null; caps are in fp16 elements.
-void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s, void* V_user,
+void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* V_user,
                   int64_t V_cap, void* M_user, int64_t M_cap, const char* fn) {
     if (!Hd->ready) {
         set_error(kErrNotInitialized, "%s: call nova_set_weights() before forward", fn);
@@ -142,50 +212,62 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s, void* V_us
         set_error(kErrInvalidArgument, "%s: null input or output pointer", fn);
         return;
     }
-    if (s.B == 0) return;
-    const uint16_t* xx = static_cast<const uint16_t*>(x);
-    uint16_t* yy = static_cast<uint16_t*>(y);
-
-    if (use_fused(Hd, s)) {
-        Hd->last_path = 2;
-        hip_ok(launch_fused(xx, Hd->U, yy, s.B, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.pad, s.nh, s.nw,
-                            s.Ho, s.Wo, Hd->stream),
-               "fused kernel");
+    if (s_all.B == 0) return;
+    const int64_t chunk = batch_chunk(Hd, s_all);
+    if (chunk < 1) {
+        set_error(kErrInvalidArgument, "%s: a single image of this shape exceeds 1 GB buffers", fn);
         return;
     }
-    if (Hd->path_pref == 2) {
-        set_error(kErrInvalidArgument, "%s: fused path unsupported for K=%d C=%d; ran 3-pass", fn,
-                  Hd->K, Hd->C);
+    const bool fused = use_fused(Hd, s_all);
+    if (!fused && Hd->path_pref == 2) {
+        set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
-    Hd->last_path = 1;
-    const int64_t needV = 64 * (int64_t)Hd->Cp * s.BP;
-    const int64_t needM = 64 * (int64_t)Hd->K * s.BP;
+    Hd->last_path = fused ? 2 : 1;
+
+    // workspace for the largest sub-batch
+    const int64_t Bc = std::min<int64_t>(chunk, s_all.B);
+    const int64_t BPc = Bc * s_all.nh * s_all.nw;
+    const int64_t needV = 64 * (int64_t)Hd->Cp * BPc;
+    const int64_t needM = 64 * (int64_t)Hd->K * BPc;
     uint16_t* V = nullptr;
     uint16_t* M = nullptr;
-    size_t ws_bytes = 0;
-    const bool userV = V_user && needV <= V_cap && aligned16(V_user);
-    const bool userM = M_user && needM <= M_cap && aligned16(M_user);
-    if (!userV) ws_bytes += (size_t)needV * 2;
-    if (!userM) ws_bytes += (size_t)needM * 2;
-    if (ws_bytes && !ensure_ws(Hd, ws_bytes)) return;
-    uint8_t* wsp = static_cast<uint8_t*>(Hd->ws);
-    if (userV) {
-        V = static_cast<uint16_t*>(V_user);
-    } else {
-        V = reinterpret_cast<uint16_t*>(wsp);
-        wsp += (size_t)needV * 2;
+    if (!fused) {
+        size_t ws_bytes = 0;
+        const bool userV = V_user && needV <= V_cap && aligned16(V_user);
+        const bool userM = M_user && needM <= M_cap && aligned16(M_user);
+        if (!userV) ws_bytes += (size_t)needV * 2;
+        if (!userM) ws_bytes += (size_t)needM * 2;
+        if (ws_bytes && !ensure_ws(Hd, ws_bytes)) return;
+        uint8_t* wsp = static_cast<uint8_t*>(Hd->ws);
+        if (userV) {
+            V = static_cast<uint16_t*>(V_user);
+        } else {
+            V = reinterpret_cast<uint16_t*>(wsp);
+            wsp += (size_t)needV * 2;
+        }
+        M = userM ? static_cast<uint16_t*>(M_user) : reinterpret_cast<uint16_t*>(wsp);
     }
-    M = userM ? static_cast<uint16_t*>(M_user) : reinterpret_cast<uint16_t*>(wsp);
 
-    if (!hip_ok(launch_input_transform(xx, V, s.B, Hd->C, s.H, s.W, s.pad, s.nh, s.nw, Hd->Cp,
-                                       (int64_t)Hd->Cp * s.BP, Hd->stream),
-                "input transform"))
-        return;
-    if (!hip_ok(launch_wgemm(Hd->U, V, M, Hd->K, Hd->Cp, (int)s.BP, Hd->stream), "wgemm"))
-        return;
-    hip_ok(launch_output_transform(M, yy, s.B, Hd->K, s.Ho, s.Wo, s.nh, s.nw, Hd->K,
-                                   (int64_t)Hd->K * s.BP, Hd->stream),
-           "output transform");
+    Profiler& pf = Hd->prof;
+    const int64_t x_img = (int64_t)Hd->C * s_all.H * s_all.W;
+    const int64_t y_img = (int64_t)Hd->K * s_all.Ho * s_all.Wo;
+    for (int64_t b0 = 0; b0 < s_all.B; b0 += chunk) {
+        Shape s = s_all;
+        s.B = (int)std::min<int64_t>(chunk, s_all.B - b0);
+        s.BP = (int64_t)s.B * s.nh * s.nw;
+        const uint16_t* xx = static_cast<const uint16_t*>(x) + b0 * x_img;
+        uint16_t* yy = static_cast<uint16_t*>(y) + b0 * y_img;
+        if (fused) {
+            const size_t e0 = pf.mark(Hd->stream);
+            if (!hip_ok(launch_fused(xx, Hd->U, yy, s.B, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.pad,
+                                     s.nh, s.nw, s.Ho, s.Wo, Hd->stream),
+                        "fused kernel"))
+                return;
+            pf.span(kKindFused, e0, pf.mark(Hd->stream), fused_name(Hd->K, Hd->C, s.BP));
+        } else if (!run_three_pass(Hd, xx, yy, s, V, M)) {
+            return;
+        }
+    }
 }
 
 }  // namespace
@@ -207,6 +289,7 @@ void nova_destroy(nova_handle_t h) {
     if (!H) return;
     if (H->U) hip_ok(hipFree(H->U), "hipFree(U)");
     if (H->ws) hip_ok(hipFree(H->ws), "hipFree(workspace)");
+    for (hipEvent_t e : H->prof.pool) hipEventDestroy(e);
     H->magic = 0;
     delete H;
 }
@@ -296,7 +379,9 @@ void nova_input_transform(const void* d_input, void* d_V_gemm, int batch, int C,
         return;
     }
     if (batch == 0) return;
-    if (nh > 65535 || (int64_t)batch * ((C + 63) / 64) > 65535) {
+    if (nh > 65535 || (int64_t)batch * ((C + 63) / 64) > 65535 ||
+        2 * (int64_t)batch * C * H * W >= ((int64_t)1 << 31) ||
+        2 * 64 * (int64_t)C * BP >= ((int64_t)1 << 31)) {
         set_error(kErrInvalidArgument, "nova_input_transform: shape exceeds launch limits");
         return;
     }
@@ -314,7 +399,9 @@ void nova_output_transform(const void* d_M_gemm, void* d_output, int batch, int 
         return;
     }
     if (batch == 0) return;
-    if (nh > 65535 || (int64_t)batch * ((K + 63) / 64) > 65535) {
+    if (nh > 65535 || (int64_t)batch * ((K + 63) / 64) > 65535 ||
+        2 * (int64_t)batch * K * H_out * W_out >= ((int64_t)1 << 31) ||
+        2 * 64 * (int64_t)K * BP >= ((int64_t)1 << 31)) {
         set_error(kErrInvalidArgument, "nova_output_transform: shape exceeds launch limits");
         return;
     }
@@ -386,7 +473,56 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     Shape s;
     if (!make_shape(Hd, batch, H, W, pad, &s, "nova_workspace_bytes")) return -1;
     if (Hd->ready && use_fused(Hd, s)) return 0;
-    return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * s.BP * 2);
+    const int64_t chunk = std::max<int64_t>(1, batch_chunk(Hd, s));
+    const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;
+    return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * BPc * 2);
+}
+
+void nova_profile_enable(nova_handle_t h, int enable) {
+    Handle* H = as_handle(h, "nova_profile_enable");
+    if (!H) return;
+    Profiler& pf = H->prof;
+    if (enable && pf.pool.empty()) {
+        const size_t n = 4 * 4096;  // 4096 three-kernel forwards between reads
+        pf.pool.reserve(n);
+        for (size_t i = 0; i < n; i++) {
+            hipEvent_t e;
+            if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) break;
+            pf.pool.push_back(e);
+        }
+    }
+    pf.on = enable != 0;
+    pf.next = 0;
+    pf.spans.clear();
+}
+
+int nova_profile_read(nova_handle_t h, double* total_ms, long long* count) {
+    Handle* H = as_handle(h, "nova_profile_read");
+    if (!H || !total_ms || !count) return -1;
+    Profiler& pf = H->prof;
+    for (int k = 0; k < kNumKinds; k++) {
+        total_ms[k] = 0.0;
+        count[k] = 0;
+    }
+    if (pf.next > 0 && !hip_ok(hipEventSynchronize(pf.pool[pf.next - 1]), "hipEventSynchronize"))
+        return -1;
+    for (const Profiler::Span& sp : pf.spans) {
+        float ms = 0.0f;
+        if (!hip_ok(hipEventElapsedTime(&ms, pf.pool[sp.e0], pf.pool[sp.e1]), "hipEventElapsedTime"))
+            return -1;
+        total_ms[sp.kind] += ms;
+        count[sp.kind] += 1;
+    }
+    const int n = (int)pf.spans.size();
+    pf.next = 0;
+    pf.spans.clear();
+    return n;
+}
+
+const char* nova_profile_kernel_name(nova_handle_t h, int kind) {
+    Handle* H = as_handle(h, "nova_profile_kernel_name");
+    if (!H || kind < 0 || kind >= kNumKinds) return "";
+    return H->prof.names[kind];
 }
 
 const char* nova_version(void) { return "nova-winograd-mi355x 0.1.0 (gfx950)"; }

@@ -52,10 +52,14 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
 // [64][BP][K].
 hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                         int BP, hipStream_t s);
+// Kernel name (template configuration) launch_wgemm picks for this shape.
+const char* wgemm_name(int K, int Cp, int BP);
 
 // ---- fused transform + GEMM + transform ------------------------------------
 // Returns false when the shape is outside the fused kernel's envelope.
 bool fused_supported(int K, int C);
+bool fused_fits(int64_t x_elems, int64_t u_elems, int64_t y_elems);
+const char* fused_name(int K, int C, int64_t BP);
 hipError_t launch_fused(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                         int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
                         int Wo, hipStream_t s);

@@ -26,6 +26,19 @@ __device__ __forceinline__ _Float16 to_f16(float v) {
     return (_Float16)v;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2. This bijection maps the dispatch index L (0..N-1) to a work index such
+// that every XCD receives one contiguous range of work items, so spatial
+// neighbours (overlapping input strips, shared cache lines) meet in the same
+// L2. Correctness does not depend on the dispatch order.
+__device__ __forceinline__ int xcd_remap(int L, int N) {
+    constexpr int kXcds = 8;
+    const int q = N / kXcds, r = N % kXcds;
+    const int xcd = L % kXcds, slot = L / kXcds;
+    const int start = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
+    return start + slot;
+}
+
 // Input tile: ld(i, j) returns d[i][j] as fp32. Processes one input column j
 // at a time, which keeps every v[r][s] chain in j order.
 template <typename Load>
@@ -53,6 +66,34 @@ __device__ __forceinline__ void input_tile(Load ld, float v[8][8]) {
 #pragma unroll
             for (int s = 0; s < 8; s++)
                 if (kBh[j][s] != 0.0f) v[r][s] = __builtin_fmaf(t[r], kBh[j][s], v[r][s]);
+    }
+}
+
+// Input tile evaluated row by row (same per-element chains as input_tile):
+// row r of T = B^T d needs all of d, row r of V needs only row r of T, so
+// only d plus two 8-vectors are live. ld(i, j) returns d[i][j] as fp32 and
+// st(r, s, v) consumes each V value.
+template <typename Load, typename Store>
+__device__ __forceinline__ void input_tile_rows(Load ld, Store st) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], ld(i, j), acc);
+            t[j] = acc;
+        }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (kBh[j][s] != 0.0f) acc = __builtin_fmaf(t[j], kBh[j][s], acc);
+            st(r, s, acc);
+        }
     }
 }
 

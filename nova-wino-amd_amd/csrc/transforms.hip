@@ -81,68 +81,115 @@ hipError_t launch_filter_transform_gemm(const float* w, uint16_t* U, int K, int 
 }
 
 // ---------------------------------------------------------------------------
-// Input transform.
-// Workgroup = one tile row (th) x kTW tiles along w x kCB channels of one
-// image. The 8 x (6*kTW+2) input strip of every channel is staged in LDS with
-// row-coalesced global loads (zero padding applied at load time); each thread
-// then transforms one (tile, channel) patch out of LDS and writes its 64
-// positions, lanes covering consecutive channels (coalesced 128 B per store).
+// Buffer-resource helpers. Every tensor is addressed through a raw buffer
+// resource: an offset at or past num_records reads 0 and drops stores, so
+// padding, tails and invalid lanes need no branches, and loads/stores take
+// their constant parts as instruction immediates or scalar offsets (no
+// per-access vector address arithmetic).
 // ---------------------------------------------------------------------------
-constexpr int kInTW = 4;                 // tiles per workgroup along w
-constexpr int kInCB = 64;                // channels per workgroup
-constexpr int kInCols = kInTW * 6 + 2;   // input columns per strip
-constexpr int kInPlane = 8 * kInCols + 2;  // halves per channel plane (odd dword stride)
+constexpr int kOob = (int)0x80000000;  // byte offset beyond any buffer used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                             (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                             0x00020000);
+}
+
+// ---------------------------------------------------------------------------
+// Input transform.
+// Workgroup = one tile row (th) x kInTW tiles along w x kInCB channels of one
+// image. Staging: each thread copies two full input rows (kInCols elements)
+// of the 8-row strip into LDS -- one vector offset per row, the column in the
+// load/store immediates; rows outside the image and channels past C read as
+// zeros through the buffer bounds. Compute: one (tile, channel) patch per
+// thread out of LDS (4-byte pair reads), 64 positions written with lanes over
+// consecutive channels (128 B per store instruction), position stride as a
+// scalar offset.
+// ---------------------------------------------------------------------------
+constexpr int kInTW = 4;                   // tiles per workgroup along w
+constexpr int kInCB = 64;                  // channels per workgroup
+constexpr int kInCols = kInTW * 6 + 2;     // 26 input columns per strip
+constexpr int kInPlane = 8 * kInCols + 2;  // 210 halves per channel (odd dword stride)
 
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
-    int nh, int nw, int ldv, int64_t pstride, int cblocks) {
-    __shared__ _Float16 sx[kInCB * kInPlane];
-    const int tw0 = blockIdx.x * kInTW;
-    const int th = blockIdx.y;
-    const int b = blockIdx.z / cblocks;
-    const int c0 = (blockIdx.z % cblocks) * kInCB;
+    int nh, int nw, int ldv, int64_t pstride, int cblocks, int64_t x_bytes, int64_t v_bytes) {
+    __shared__ __align__(16) _Float16 sx[kInCB * kInPlane];
+    // 1-D grid over (tile block, tile row, image x channel block), x fastest
+    const int nwb = (nw + kInTW - 1) / kInTW;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int tw0 = (L % nwb) * kInTW;
+    const int th = (L / nwb) % nh;
+    const int bz = L / (nwb * nh);
+    const int b = bz / cblocks;
+    const int c0 = (bz % cblocks) * kInCB;
     const int h0 = th * 6 - pad, w0 = tw0 * 6 - pad;
-    const _Float16* xb = x + (int64_t)b * C * H * W;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, x_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
 
-    for (int idx = threadIdx.x; idx < kInCB * 8 * kInCols; idx += 256) {
-        const int cc = idx / (8 * kInCols);
-        const int rem = idx - cc * (8 * kInCols);
-        const int i = rem / kInCols;
-        const int j = rem - i * kInCols;
-        const int c = c0 + cc, h = h0 + i, ww = w0 + j;
-        _Float16 v = (_Float16)0.0f;
-        if (c < C && h >= 0 && h < H && ww >= 0 && ww < W) v = xb[((int64_t)c * H + h) * W + ww];
-        sx[cc * kInPlane + i * kInCols + j] = v;
+    // ---- staging: thread (row i, column col) copies its element for all 64
+    // channels. Lanes run along the row (two rows per wave: each load covers
+    // two 52-byte runs), the channel stride is a scalar offset, and row /
+    // column validity is folded into the vector offset (out of range -> 0). ----
+    {
+        const int i = threadIdx.x >> 5, col = threadIdx.x & 31;
+        if (col < kInCols) {
+            const int h = h0 + i, w = w0 + col;
+            const bool ok = h >= 0 && h < H && w >= 0 && w < W;
+            const int voff = ok ? 2 * (((b * C + c0) * H + h) * W + w) : kOob;
+            const int HW2 = 2 * H * W;
+            const int ncc = min(kInCB, C - c0);  // uniform
+            _Float16* sdst = sx + i * kInCols + col;
+            uint16_t v[kInCB];
+            if (ncc == kInCB) {  // full channel block: all 64 loads in flight at once
+#pragma unroll
+                for (int u = 0; u < kInCB; u++)
+                    v[u] = __builtin_amdgcn_raw_buffer_load_b16(xrs, voff, u * HW2, 0);
+            } else {
+#pragma unroll
+                for (int u = 0; u < kInCB; u++)
+                    v[u] = u < ncc ? __builtin_amdgcn_raw_buffer_load_b16(xrs, voff, u * HW2, 0)
+                                   : (uint16_t)0;
+            }
+#pragma unroll
+            for (int u = 0; u < kInCB; u++) sdst[u * kInPlane] = __builtin_bit_cast(_Float16, v[u]);
+        }
     }
     __syncthreads();
 
+    // ---- compute: (tile t, channel cc) per thread ----
     const int cc = threadIdx.x & 63;
     const int t = threadIdx.x >> 6;
     const int tw = tw0 + t;
     const int c = c0 + cc;
-    if (tw >= nw || c >= ldv) return;
-    const int64_t bp = ((int64_t)b * nh + th) * nw + tw;
-    _Float16* out = V + bp * ldv + c;
-    if (c >= C) {  // zero padding of the channel pitch
-#pragma unroll
-        for (int p = 0; p < 64; p++) out[p * pstride] = (_Float16)0.0f;
-        return;
-    }
+    const int bp = (b * nh + th) * nw + tw;
+    const int voff = (tw < nw && c < ldv) ? 2 * (bp * ldv + c) : kOob;
     const _Float16* sp = sx + cc * kInPlane + t * 6;
-    float v[8][8];
-    input_tile([&](int i, int j) { return (float)sp[i * kInCols + j]; }, v);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 d2[8][4];
 #pragma unroll
-    for (int p = 0; p < 64; p++) out[p * pstride] = to_f16(v[p >> 3][p & 7]);
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+            d2[i][jj] = *reinterpret_cast<const h2*>(sp + i * kInCols + 2 * jj);
+    input_tile_rows([&](int i, int j) { return (float)d2[i][j >> 1][j & 1]; },
+                    [&](int r, int s, float v) {
+                        const int p = r * 8 + s;
+                        __builtin_amdgcn_raw_buffer_store_b16(
+                            __builtin_bit_cast(uint16_t, to_f16(v)), vrs, voff,
+                            (int)(2 * p * pstride), 0);
+                    });
 }
 
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
                                   hipStream_t s) {
     const int cblocks = (ldv + kInCB - 1) / kInCB;
-    dim3 grid((unsigned)((nw + kInTW - 1) / kInTW), (unsigned)nh, (unsigned)(B * cblocks));
-    input_transform_kernel<<<grid, dim3(256), 0, s>>>(
+    const int64_t nblocks = (int64_t)((nw + kInTW - 1) / kInTW) * nh * B * cblocks;
+    if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
+    input_transform_kernel<<<dim3((unsigned)nblocks), dim3(256), 0, s>>>(
         reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad, nh,
-        nw, ldv, pstride, cblocks);
+        nw, ldv, pstride, cblocks, 2 * (int64_t)B * C * H * W, 2 * 64 * pstride);
     return hipGetLastError();
 }
 
@@ -150,32 +197,45 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
 // Output transform.
 // Workgroup = one tile row x kOutTW tiles x kOutKB output channels of one
 // image. Each thread reads the 64 positions of one (tile, k) (lanes over
-// consecutive k: coalesced), computes the 6x6 tile, parks it in LDS, and the
-// workgroup then writes the tile row's output rows with w-contiguous stores.
+// consecutive k: coalesced; position stride as a scalar offset), computes the
+// 6x6 tile into LDS; the workgroup then writes whole output rows (one vector
+// offset per row, the column in the store immediate). Rows past Ho and
+// channels past K fall outside the buffer and are dropped; columns past Wo
+// are skipped with a workgroup-uniform bound.
 // ---------------------------------------------------------------------------
 constexpr int kOutTW = 4;
 constexpr int kOutKB = 64;
-constexpr int kOutCols = kOutTW * 6;
+constexpr int kOutCols = kOutTW * 6;         // 24
 constexpr int kOutPlane = 6 * kOutCols + 2;  // 146 halves = 73 dwords (odd)
 
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
-    int nw, int ldm, int64_t pstride, int kblocks) {
-    __shared__ _Float16 sy[kOutKB * kOutPlane];
-    const int tw0 = blockIdx.x * kOutTW;
-    const int th = blockIdx.y;
-    const int b = blockIdx.z / kblocks;
-    const int k0 = (blockIdx.z % kblocks) * kOutKB;
+    int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes) {
+    __shared__ __align__(16) _Float16 sy[kOutKB * kOutPlane];
+    const int nwb = (nw + kOutTW - 1) / kOutTW;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int tw0 = (L % nwb) * kOutTW;
+    const int th = (L / nwb) % nh;
+    const int bz = L / (nwb * nh);
+    const int b = bz / kblocks;
+    const int k0 = (bz % kblocks) * kOutKB;
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, m_bytes);
+    const __amdgpu_buffer_rsrc_t yrs = make_rsrc(y, y_bytes);
 
-    const int kk = threadIdx.x & 63;
-    const int t = threadIdx.x >> 6;
-    const int tw = tw0 + t;
-    const int k = k0 + kk;
-    if (tw < nw && k < K) {
-        const int64_t bp = ((int64_t)b * nh + th) * nw + tw;
-        const _Float16* mp = M + bp * ldm + k;
+    {
+        const int kk = threadIdx.x & 63;
+        const int t = threadIdx.x >> 6;
+        const int tw = tw0 + t;
+        const int k = k0 + kk;
+        const int bp = (b * nh + th) * nw + tw;
+        const int moff = (tw < nw && k < K) ? 2 * (bp * ldm + k) : kOob;
+        uint16_t m[64];
+#pragma unroll
+        for (int p = 0; p < 64; p++)
+            m[p] = __builtin_amdgcn_raw_buffer_load_b16(mrs, moff, (int)(2 * p * pstride), 0);
         float out[6][6];
-        output_tile([&](int i, int j) { return (float)mp[(i * 8 + j) * pstride]; }, out);
+        output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
+                    out);
         _Float16* sp = sy + kk * kOutPlane + t * 6;
 #pragma unroll
         for (int r = 0; r < 6; r++)
@@ -184,15 +244,27 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     }
     __syncthreads();
 
-    const int wbase = tw0 * 6;
-    for (int idx = threadIdx.x; idx < kOutKB * 6 * kOutCols; idx += 256) {
-        const int q = idx / (6 * kOutCols);
-        const int rem = idx - q * (6 * kOutCols);
-        const int r = rem / kOutCols;
-        const int col = rem - r * kOutCols;
-        const int kq = k0 + q, h = th * 6 + r, ww = wbase + col;
-        if (kq < K && h < Ho && ww < Wo && (col / 6) + tw0 < nw)
-            y[(((int64_t)b * K + kq) * Ho + h) * Wo + ww] = sy[q * kOutPlane + r * kOutCols + col];
+    // ---- store: thread (row r, column col) writes its element for all 64
+    // channels: lanes run along the output row (two rows per wave), the
+    // channel stride is a scalar offset; rows past Ho / columns past the
+    // tile block or Wo fall outside and are dropped. ----
+    {
+        const int r = threadIdx.x >> 5, col = threadIdx.x & 31;
+        const int h = th * 6 + r, w = tw0 * 6 + col;
+        const int ncols = min(kOutCols, (nw - tw0) * 6);  // uniform
+        if (r < 6 && col < ncols) {
+            const bool ok = h < Ho && w < Wo;
+            const int yoff = ok ? 2 * (((b * K + k0) * Ho + h) * Wo + w) : kOob;
+            const int HoWo2 = 2 * Ho * Wo;
+            const int nkk = min(kOutKB, K - k0);  // uniform
+            const _Float16* ssrc = sy + r * kOutCols + col;
+#pragma unroll 16
+            for (int u = 0; u < kOutKB; u++) {
+                if (u < nkk)
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        __builtin_bit_cast(uint16_t, ssrc[u * kOutPlane]), yrs, yoff, u * HoWo2, 0);
+            }
+        }
     }
 }
 
@@ -200,10 +272,11 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
                                    hipStream_t s) {
     const int kblocks = (K + kOutKB - 1) / kOutKB;
-    dim3 grid((unsigned)((nw + kOutTW - 1) / kOutTW), (unsigned)nh, (unsigned)(B * kblocks));
-    output_transform_kernel<<<grid, dim3(256), 0, s>>>(
+    const int64_t nblocks = (int64_t)((nw + kOutTW - 1) / kOutTW) * nh * B * kblocks;
+    if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
+    output_transform_kernel<<<dim3((unsigned)nblocks), dim3(256), 0, s>>>(
         reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
-        ldm, pstride, kblocks);
+        ldm, pstride, kblocks, 2 * 64 * pstride, 2 * (int64_t)B * K * Ho * Wo);
     return hipGetLastError();
 }
 

@@ -13,6 +13,7 @@
 // accumulator lane holds D[4*(l/16) + i][l % 16]. The channel pitch Cp is a
 // multiple of 8 and zero padded, so partial 32-channel steps only mask whole
 // 8-channel groups. No atomics, no split-K: results are deterministic.
+// Byte offsets are 32-bit: U, V and M must each stay below 2 GB.
 #include "nova_internal.h"
 
 namespace nova {
@@ -20,9 +21,23 @@ namespace nova {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
-// MT x NT 16x16 MFMA tiles per wave, WGM x WGN waves per workgroup.
-template <int MT, int NT, int WGM, int WGN>
+constexpr int kOob = (int)0x80000000;  // byte offset past every buffer: loads 0, stores dropped
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                             (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                             0x00020000);
+}
+
+// MT x NT 16x16 MFMA tiles per wave, WGM x WGN waves per workgroup. Operands
+// are read through buffer resources: the per-lane part of each offset (row,
+// channel octet) is fixed, the wave-uniform part (position, channel step)
+// goes in a scalar offset, and lanes outside K / BP / Cp read zeros. A ring
+// of PD channel steps is kept in flight (register prefetch) so the loop is
+// not bound by load latency; steps past Cp are zero loads.
+template <int MT, int NT, int WGM, int WGN, int PD>
 __global__ __launch_bounds__(64 * WGM * WGN) void wgemm_kernel(
     const _Float16* __restrict__ U, const _Float16* __restrict__ V, _Float16* __restrict__ M,
     int K, int Cp, int BP) {
@@ -35,25 +50,38 @@ __global__ __launch_bounds__(64 * WGM * WGN) void wgemm_kernel(
     const int r16 = lane & 15;
     const int g = lane >> 4;
 
-    const _Float16* Up = U + (int64_t)p * K * Cp;
-    const _Float16* Vp = V + (int64_t)p * BP * Cp;
+    const __amdgpu_buffer_rsrc_t urs = make_rsrc(U, 2 * (int64_t)64 * K * Cp);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, 2 * (int64_t)64 * BP * Cp);
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, 2 * (int64_t)64 * BP * K);
 
-    const _Float16* arow[MT];
-    bool aok[MT];
+    int aoff[MT], boff[NT];
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         const int k = kbase + mi * 16 + r16;
-        aok[mi] = k < K;
-        arow[mi] = Up + (int64_t)(aok[mi] ? k : 0) * Cp + 8 * g;
+        aoff[mi] = k < K ? 2 * (k * Cp + 8 * g) : kOob;
     }
-    const _Float16* brow[NT];
-    bool bok[NT];
 #pragma unroll
     for (int ni = 0; ni < NT; ni++) {
         const int n = nbase + ni * 16 + r16;
-        bok[ni] = n < BP;
-        brow[ni] = Vp + (int64_t)(bok[ni] ? n : 0) * Cp + 8 * g;
+        boff[ni] = n < BP ? 2 * (n * Cp + 8 * g) : kOob;
     }
+    const int au = 2 * p * K * Cp;   // uniform
+    const int bu = 2 * p * BP * Cp;  // uniform
+    const int nsteps = (Cp + 31) / 32;
+
+    h8 a[PD][MT], b[PD][NT];
+    auto load_step = [&](int step, h8 af[MT], h8 bf[NT]) {
+        const int c = step * 32;
+        const bool cok = c + 8 * g < Cp;
+#pragma unroll
+        for (int mi = 0; mi < MT; mi++)
+            af[mi] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                urs, cok ? aoff[mi] : kOob, au + 2 * c, 0));
+#pragma unroll
+        for (int ni = 0; ni < NT; ni++)
+            bf[ni] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                vrs, cok ? boff[ni] : kOob, bu + 2 * c, 0));
+    };
 
     f4 acc[MT][NT];
 #pragma unroll
@@ -61,26 +89,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) void wgemm_kernel(
 #pragma unroll
         for (int ni = 0; ni < NT; ni++) acc[mi][ni] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const h8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll 2
-    for (int c = 0; c < Cp; c += 32) {
-        const bool cok = c + 8 * g < Cp;
-        h8 a[MT], b[NT];
 #pragma unroll
-        for (int mi = 0; mi < MT; mi++)
-            a[mi] = (aok[mi] && cok) ? *reinterpret_cast<const h8*>(arow[mi] + c) : zero8;
+    for (int j = 0; j < PD; j++) load_step(j, a[j], b[j]);
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
 #pragma unroll
-        for (int ni = 0; ni < NT; ni++)
-            b[ni] = (bok[ni] && cok) ? *reinterpret_cast<const h8*>(brow[ni] + c) : zero8;
+        for (int j = 0; j < PD; j++) {
 #pragma unroll
-        for (int mi = 0; mi < MT; mi++)
+            for (int mi = 0; mi < MT; mi++)
 #pragma unroll
-            for (int ni = 0; ni < NT; ni++)
-                acc[mi][ni] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
+                for (int ni = 0; ni < NT; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][mi], b[j][ni],
+                                                                         acc[mi][ni], 0, 0, 0);
+            if (s0 + PD < nsteps) load_step(s0 + PD + j, a[j], b[j]);
+        }
     }
 
-    _Float16* Mp = M + (int64_t)p * BP * K;
+    const int mu = 2 * p * BP * K;  // uniform
     const bool vec_store = (K & 3) == 0;
 #pragma unroll
     for (int mi = 0; mi < MT; mi++)
@@ -88,36 +112,213 @@ __global__ __launch_bounds__(64 * WGM * WGN) void wgemm_kernel(
         for (int ni = 0; ni < NT; ni++) {
             const int bp = nbase + ni * 16 + r16;
             const int k = kbase + mi * 16 + 4 * g;
-            if (bp >= BP) continue;
-            _Float16* dst = Mp + (int64_t)bp * K + k;
-            if (vec_store && k + 3 < K) {
+            const int off = bp < BP ? 2 * (bp * K + k) : kOob;
+            if (vec_store) {
                 h4 v = {(_Float16)acc[mi][ni][0], (_Float16)acc[mi][ni][1],
                         (_Float16)acc[mi][ni][2], (_Float16)acc[mi][ni][3]};
-                *reinterpret_cast<h4*>(dst) = v;
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, v), mrs,
+                                                      k < K ? off : kOob, mu, 0);
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    if (k + i < K) dst[i] = (_Float16)acc[mi][ni][i];
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[mi][ni][i]), mrs,
+                        k + i < K ? off + 2 * i : kOob, mu, 0);
             }
         }
 }
 
-template <int MT, int NT, int WGM, int WGN>
+template <int MT, int NT, int WGM, int WGN, int PD>
 static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                              int BP, hipStream_t s) {
     constexpr int TM = MT * 16 * WGM, TN = NT * 16 * WGN;
     dim3 grid((unsigned)((BP + TN - 1) / TN), (unsigned)((K + TM - 1) / TM), 64);
-    wgemm_kernel<MT, NT, WGM, WGN><<<grid, dim3(64 * WGM * WGN), 0, s>>>(
+    wgemm_kernel<MT, NT, WGM, WGN, PD><<<grid, dim3(64 * WGM * WGN), 0, s>>>(
         reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
         reinterpret_cast<_Float16*>(M), K, Cp, BP);
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// LDS-tiled variant for larger shapes. Workgroup tile = TK output channels x
+// TB tiles (bp) of one position, 4 waves (WK x WB), channels in stages of 64
+// (two MFMA k-steps): every stage is copied global -> registers -> LDS with
+// 16-byte loads (one 128-byte line per row when Cp >= 64), double buffered so
+// the next stage's loads are in flight while the current one is multiplied.
+// LDS rows are padded to 72 halves (144 B = 36 banks), which makes the
+// 16-byte fragment reads of 8 consecutive lanes hit 8 disjoint bank groups.
+// ---------------------------------------------------------------------------
+constexpr int kStageC = 64;
+constexpr int kPitch = 72;
+
+template <int TK, int TB, int WK, int WB>
+__global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restrict__ U,
+                                                        const _Float16* __restrict__ V,
+                                                        _Float16* __restrict__ M, int K, int Cp,
+                                                        int BP) {
+    static_assert(WK * WB == 4, "4 waves");
+    constexpr int MT = TK / WK / 16;  // 16x16 tiles per wave along k
+    constexpr int NT = TB / WB / 16;  // along bp
+    constexpr int kChunksU = TK * kStageC / 8;  // 16-byte chunks per stage
+    constexpr int kChunksV = TB * kStageC / 8;
+    constexpr int kPerThreadU = (kChunksU + 255) / 256;
+    constexpr int kPerThreadV = (kChunksV + 255) / 256;
+    __shared__ __align__(16) _Float16 sU[2][TK * kPitch];
+    __shared__ __align__(16) _Float16 sV[2][TB * kPitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wk = wave % WK, wb = wave / WK;
+    const int p = blockIdx.z;
+    const int k0 = blockIdx.y * TK;
+    const int n0 = blockIdx.x * TB;
+    const int r16 = lane & 15, g = lane >> 4;
+
+    const __amdgpu_buffer_rsrc_t urs = make_rsrc(U, 2 * (int64_t)64 * K * Cp);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, 2 * (int64_t)64 * BP * Cp);
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, 2 * (int64_t)64 * BP * K);
+    const int au = 2 * p * K * Cp;  // uniform byte offsets of position p
+    const int bu = 2 * p * BP * Cp;
+
+    // staging assignment: chunk id -> (row, 8-channel group); 8 chunks per row
+    int uoff[kPerThreadU], ulds[kPerThreadU], voff[kPerThreadV], vlds[kPerThreadV];
+#pragma unroll
+    for (int j = 0; j < kPerThreadU; j++) {
+        const int ch = tid + j * 256;
+        const int row = ch >> 3, cg = ch & 7;
+        const bool ok = ch < kChunksU && k0 + row < K;
+        uoff[j] = ok ? 2 * ((k0 + row) * Cp + cg * 8) : kOob;
+        ulds[j] = ch < kChunksU ? row * kPitch + cg * 8 : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kPerThreadV; j++) {
+        const int ch = tid + j * 256;
+        const int row = ch >> 3, cg = ch & 7;
+        const bool ok = ch < kChunksV && n0 + row < BP;
+        voff[j] = ok ? 2 * ((n0 + row) * Cp + cg * 8) : kOob;
+        vlds[j] = ch < kChunksV ? row * kPitch + cg * 8 : -1;
+    }
+    const int nstages = (Cp + kStageC - 1) / kStageC;
+    h8 ru[kPerThreadU], rv[kPerThreadV];
+    auto gload = [&](int st) {
+        const int c = st * kStageC;
+#pragma unroll
+        for (int j = 0; j < kPerThreadU; j++) {
+            const int cg = (tid + j * 256) & 7;
+            const bool cok = c + cg * 8 < Cp;
+            ru[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               urs, cok ? uoff[j] : kOob, au + 2 * c, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < kPerThreadV; j++) {
+            const int cg = (tid + j * 256) & 7;
+            const bool cok = c + cg * 8 < Cp;
+            rv[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               vrs, cok ? voff[j] : kOob, bu + 2 * c, 0));
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < kPerThreadU; j++)
+            if (ulds[j] >= 0) *reinterpret_cast<h8*>(&sU[buf][ulds[j]]) = ru[j];
+#pragma unroll
+        for (int j = 0; j < kPerThreadV; j++)
+            if (vlds[j] >= 0) *reinterpret_cast<h8*>(&sV[buf][vlds[j]]) = rv[j];
+    };
+
+    f4 acc[MT][NT];
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NT; ni++) acc[mi][ni] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int st = 0; st < nstages; st++) {
+        const int buf = st & 1;
+        if (st + 1 < nstages) gload(st + 1);
+        const _Float16* su = sU[buf] + (wk * MT * 16 + r16) * kPitch + 8 * g;
+        const _Float16* sv = sV[buf] + (wb * NT * 16 + r16) * kPitch + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < kStageC / 32; kk++) {
+            h8 a[MT], b[NT];
+#pragma unroll
+            for (int mi = 0; mi < MT; mi++)
+                a[mi] = *reinterpret_cast<const h8*>(su + mi * 16 * kPitch + kk * 32);
+#pragma unroll
+            for (int ni = 0; ni < NT; ni++)
+                b[ni] = *reinterpret_cast<const h8*>(sv + ni * 16 * kPitch + kk * 32);
+#pragma unroll
+            for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+                for (int ni = 0; ni < NT; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mi], b[ni],
+                                                                         acc[mi][ni], 0, 0, 0);
+        }
+        if (st + 1 < nstages) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    const int mu = 2 * p * BP * K;
+    const bool vec_store = (K & 3) == 0;
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+        for (int ni = 0; ni < NT; ni++) {
+            const int bp = n0 + (wb * NT + ni) * 16 + r16;
+            const int k = k0 + (wk * MT + mi) * 16 + 4 * g;
+            const int off = bp < BP ? 2 * (bp * K + k) : kOob;
+            if (vec_store) {
+                h4 v = {(_Float16)acc[mi][ni][0], (_Float16)acc[mi][ni][1],
+                        (_Float16)acc[mi][ni][2], (_Float16)acc[mi][ni][3]};
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, v), mrs,
+                                                      k < K ? off : kOob, mu, 0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[mi][ni][i]), mrs,
+                        k + i < K ? off + 2 * i : kOob, mu, 0);
+            }
+        }
+}
+
+template <int TK, int TB, int WK, int WB>
+static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
+                             int BP, hipStream_t s) {
+    dim3 grid((unsigned)((BP + TB - 1) / TB), (unsigned)((K + TK - 1) / TK), 64);
+    wgemm_lds_kernel<TK, TB, WK, WB><<<grid, dim3(256), 0, s>>>(
+        reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
+        reinterpret_cast<_Float16*>(M), K, Cp, BP);
+    return hipGetLastError();
+}
+
+// Kernel per shape: register-direct 64 x 16 for GEMV-like B=1 deep layers
+// (few tiles), LDS-tiled otherwise -- 128 x 128 when both K and BP are large,
+// 64 x 64 when either is small.
+static int wgemm_cfg(int K, int BP) {
+    if (BP <= 16) return 0;
+    if (K >= 128 && BP >= 128) return 2;
+    return 1;
+}
+
+const char* wgemm_name(int K, int Cp, int BP) {
+    (void)Cp;
+    static const char* names[] = {"wgemm_kernel<1, 1, 4, 1, 4>",
+                                  "wgemm_lds_kernel<64, 64, 2, 2>",
+                                  "wgemm_lds_kernel<128, 128, 2, 2>"};
+    return names[wgemm_cfg(K, BP)];
+}
+
 hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                         int BP, hipStream_t s) {
-    if (BP <= 16) return launch_cfg<1, 1, 4, 1>(U, V, M, K, Cp, BP, s);   // 64 x 16
-    if (BP <= 64) return launch_cfg<1, 2, 4, 1>(U, V, M, K, Cp, BP, s);   // 64 x 32
-    return launch_cfg<2, 2, 2, 2>(U, V, M, K, Cp, BP, s);                 // 64 x 64
+    switch (wgemm_cfg(K, BP)) {
+        case 0: return launch_cfg<1, 1, 4, 1, 4>(U, V, M, K, Cp, BP, s);
+        case 1: return launch_lds<64, 64, 2, 2>(U, V, M, K, Cp, BP, s);
+        default: return launch_lds<128, 128, 2, 2>(U, V, M, K, Cp, BP, s);
+    }
 }
 
 }  // namespace nova

@@ -55,6 +55,10 @@ _SIGNATURES = {
     "nova_set_path": (None, [_vp, _i]),
     "nova_get_last_path": (_i, [_vp]),
     "nova_workspace_bytes": (ctypes.c_longlong, [_vp, _i, _i, _i, _i]),
+    "nova_profile_enable": (None, [_vp, _i]),
+    "nova_profile_read": (_i, [_vp, ctypes.POINTER(ctypes.c_double),
+                               ctypes.POINTER(ctypes.c_longlong)]),
+    "nova_profile_kernel_name": (ctypes.c_char_p, [_vp, _i]),
     "nova_version": (ctypes.c_char_p, []),
 }
 

@@ -119,7 +119,8 @@ def test_output_transform_bitexact(oracle, B, K, Ho, Wo):
 
 
 GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256, 28),
-              (1, 256, 256, 14), (1, 16, 40, 9)]
+              (1, 256, 256, 14), (1, 16, 40, 9), (8, 128, 128, 28), (2, 136, 200, 30),
+              (4, 72, 132, 40)]
 
 
 @pytest.mark.parametrize("B,C,K,H", GEMM_CASES)
@@ -172,6 +173,8 @@ def test_gemm_within_fp32_bound(oracle, B, C, K, H):
 FORWARD_CASES = [
     # (B, C, K, H, W, pad) -- BASELINE configs 1-2 and edge shapes
     (1, 64, 64, 56, 56, 1),
+    (4, 64, 64, 56, 56, 1),
+    (3, 32, 96, 20, 20, 1),
     (1, 128, 128, 28, 28, 1),
     (1, 256, 256, 14, 14, 1),
     (1, 512, 512, 7, 7, 1),
@@ -207,10 +210,12 @@ def _forward_case(oracle, B, C, K, H, W, pad, path):
     return yg, yo, truth, took
 
 
+@pytest.mark.parametrize("path", [1, 2], ids=["3pass", "fused"])
 @pytest.mark.parametrize("B,C,K,H,W,pad", FORWARD_CASES)
-def test_forward_matches_oracle(oracle, B, C, K, H, W, pad):
-    print(f"[forward] B={B} C={C} K={K} H={H} W={W} pad={pad}", flush=True)
-    yg, yo, truth, _ = _forward_case(oracle, B, C, K, H, W, pad, 0)
+def test_forward_matches_oracle(oracle, B, C, K, H, W, pad, path):
+    print(f"[forward] B={B} C={C} K={K} H={H} W={W} pad={pad} path={path}", flush=True)
+    yg, yo, truth, took = _forward_case(oracle, B, C, K, H, W, pad, path)
+    assert took == path
     assert np.isfinite(yg.astype(np.float32)).all()
     rel = oracle.rel_l2(yg, yo)
     assert rel <= 5e-3, rel
