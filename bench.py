@@ -17,7 +17,8 @@ Reported on one JSON line (stdout):
                T_roof/T (T_roof = max(2*64*K*C*B*P_min / 2.5 PF,
                (2BCHW + 2BKHoWo + 2*64*K*C) / 8 TB/s))
   roofline     the dominant kernel of the step (largest summed time), timed
-               live with the library's hipEvents on its launch stream:
+               live: the library re-launches each kernel of each layer back to
+               back with one hipEvent pair on its launch stream around the loop;
                algorithmic bytes per launch / average launch time vs 8 TB/s
   cpu_baseline the CPU oracle (the reference's NOVA arithmetic, C, OpenMP) on
                a bounded sample of the same layers, on this host's cores
@@ -111,18 +112,74 @@ def graph_of(fn, torch):
         return None
 
 
-def load_traffic(kernel_name, layer_desc):
-    """HBM bytes per launch measured offline with rocprofv3 FETCH_SIZE /
-    WRITE_SIZE (profiles/traffic.json), or None."""
+def load_traffic(kernel_name):
+    """HBM bytes per launch (mean over the step's layers) measured offline with
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         data = json.load(f)
     for rec in data.get("kernels", []):
-        if rec.get("kernel") == kernel_name and rec.get("workload") == layer_desc:
+        if rec.get("kernel") == kernel_name:
             return rec.get("hbm_bytes_per_launch")
     return None
+
+
+COPY_MIB = 256
+
+
+def pmc_workload(runs, reps, torch):
+    """Short run for rocprofv3 --pmc passes: one plain device copy of a known
+    size (the FETCH_SIZE/WRITE_SIZE calibration) and a few forwards per layer."""
+    n = COPY_MIB * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    for r in runs:
+        for _ in range(reps):
+            r["mod"](r["x"])
+    torch.cuda.synchronize()
+
+
+def traffic_from(fetch_dir, write_dir, out_path, kernel_name):
+    """HBM bytes per launch of `kernel_name` from two rocprofv3 --pmc runs of
+    `bench.py --pmc-mode` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
+    scaled by the same counter's reading for the known-size copy kernel."""
+    import glob
+    import sqlite3
+
+    def read(d, counter):
+        db = sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True))[-1]
+        con = sqlite3.connect(db)
+        rows = con.execute("select kernel_name, grid_size, avg(value), count(*) from "
+                           "counters_collection where counter_name = ? group by kernel_name, "
+                           "grid_size", (counter,)).fetchall()
+        copy = [r for r in rows if "copy" in r[0].lower() and r[1] >= COPY_MIB * (1 << 20) // 16]
+        kern = [r for r in rows if kernel_name in r[0]]
+        if not copy or not kern:
+            raise SystemExit(f"{counter}: copy kernel or {kernel_name} not found in {db}")
+        copy_kib = max(copy, key=lambda r: r[1])[2]
+        mean_kib = sum(r[2] for r in kern) / len(kern)  # one launch per layer
+        factor = COPY_MIB * 1024.0 / copy_kib
+        return mean_kib * 1024.0 * factor, factor, [(r[1], r[2]) for r in kern]
+
+    fetch, ff, fk = read(fetch_dir, "FETCH_SIZE")
+    write, wf, wk = read(write_dir, "WRITE_SIZE")
+    rec = {"kernel": kernel_name, "hbm_bytes_per_launch": round(fetch + write),
+           "fetch_bytes_per_launch": round(fetch), "write_bytes_per_launch": round(write),
+           "fetch_scale": round(ff, 4), "write_scale": round(wf, 4),
+           "copy_calibration_bytes": COPY_MIB * (1 << 20),
+           "per_grid_kib": {"fetch": fk, "write": wk}}
+    data = {"kernels": []}
+    if os.path.exists(out_path):
+        with open(out_path) as f:
+            data = json.load(f)
+    data["kernels"] = [k for k in data["kernels"] if k.get("kernel") != kernel_name] + [rec]
+    with open(out_path, "w") as f:
+        json.dump(data, f, indent=1)
+    print(json.dumps(rec))
 
 
 def cpu_baseline(layers_spec, budget_s, threads):
@@ -195,12 +252,23 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layer-reps", type=int, default=200)
+    ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-miopen", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--details", default="", help="write the full per-layer report here")
+    ap.add_argument("--pmc-mode", action="store_true",
+                    help="short run for rocprofv3 --pmc passes (copy calibration + forwards)")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two --pmc-mode profiles into profiles/traffic.json and exit")
+    ap.add_argument("--traffic-kernel", default="input_transform_kernel")
     args = ap.parse_args()
+
+    if args.traffic_from:
+        traffic_from(args.traffic_from[0], args.traffic_from[1],
+                     os.path.join(ROOT, "profiles", "traffic.json"), args.traffic_kernel)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -242,6 +310,12 @@ def main():
         for r in runs:
             r["mod"](r["x"])
 
+    if args.pmc_mode:
+        with torch.no_grad():
+            step()
+            pmc_workload(runs, 3, torch)
+        return
+
     with torch.no_grad():
         # warm-up (filter transforms, workspaces, MIOpen solution search)
         for _ in range(args.warmup):
@@ -260,36 +334,36 @@ def main():
         ms_per_step = (t1 - t0) * 1e3 / args.steps
         value = total_flops / (ms_per_step * 1e-3) / 1e12
 
-        # ---- per-kernel timing over a second K-step region ----------------------
-        for r in runs:
-            lib.nova_profile_enable(r["mod"]._handle.h, 1)
-        for _ in range(args.steps):
-            step()
-        import ctypes
-
+        # ---- per-kernel timing: each kernel of each layer's forward is
+        # re-launched back to back by the library (nova_profile_replay) with one
+        # hipEvent pair on its own stream around the loop -> mean launch time.
+        # (Event pairs around single launches would add the command processor's
+        # per-packet overhead to short kernels.)
         kernels = {}
         for r in runs:
-            tot = (ctypes.c_double * 4)()
-            cnt = (ctypes.c_longlong * 4)()
+            y_keep = r["mod"](r["x"])  # the forward whose launches are replayed
             h = r["mod"]._handle.h
-            lib.nova_profile_read(h, tot, cnt)
             r["kernels"] = {}
             for k in range(4):
-                if cnt[k] == 0:
-                    continue
                 kname = lib.nova_profile_kernel_name(h, k).decode()
-                per = tot[k] / cnt[k]
+                if not kname:
+                    continue
+                per = lib.nova_profile_replay(h, k, args.kernel_reps)
+                if per < 0:
+                    lib.nova_get_last_error()  # kind not launched by this path
+                    continue
                 ab = kernel_alg_bytes(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"])
                 r["kernels"][KIND_NAMES[k]] = {"kernel": kname, "avg_us": per * 1e3,
                                               "alg_bytes": ab,
                                               "gbs": ab / (per * 1e-3) / 1e9}
                 agg = kernels.setdefault(kname, {"ms": 0.0, "launches": 0, "bytes": 0.0,
                                                  "by_layer": []})
-                agg["ms"] += tot[k]
-                agg["launches"] += cnt[k]
-                agg["bytes"] += ab * cnt[k]
+                agg["ms"] += per
+                agg["launches"] += 1
+                agg["bytes"] += ab
                 agg["by_layer"].append(f"{r['name']}_b{r['B']}")
-            lib.nova_profile_enable(h, 0)
+            torch.cuda.synchronize()
+            del y_keep
 
         # ---- per-layer timings: NOVA vs MIOpen, eager and graph -----------------
         for r in runs:
@@ -310,7 +384,7 @@ def main():
     # ---- dominant kernel roofline -----------------------------------------------
     dom_name, dom = max(kernels.items(), key=lambda kv: kv[1]["ms"])
     avg_s = dom["ms"] / dom["launches"] * 1e-3
-    bytes_per_launch = dom["bytes"] / dom["launches"]
+    bytes_per_launch = dom["bytes"] / dom["launches"]  # launches: one per layer per step
     achieved = bytes_per_launch / avg_s / 1e9
     dom_desc = ",".join(sorted(set(dom["by_layer"])))
     roofline = {
@@ -319,11 +393,11 @@ def main():
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBS, 4),
-        "traffic": load_traffic(dom_name, dom_desc),
+        "traffic": load_traffic(dom_name),
         "kernel": dom_name,
         "avg_launch_us": round(avg_s * 1e6, 3),
         "alg_bytes_per_launch": round(bytes_per_launch),
-        "launches_per_step": dom["launches"] // args.steps,
+        "launches_per_step": dom["launches"],
         "share_of_kernel_time": round(dom["ms"] / sum(v["ms"] for v in kernels.values()), 3),
         "layers": dom_desc,
     }

@@ -127,6 +127,12 @@ NOVA_API long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W
  * transform, 3 fused) and resets. Returns the number of timed launches. */
 NOVA_API void nova_profile_enable(nova_handle_t h, int enable);
 NOVA_API int nova_profile_read(nova_handle_t h, double* total_ms, long long* count);
+/* Re-launches the kernel of `kind` from the handle's most recent forward
+ * (first sub-batch) `reps` times back to back on the handle's stream, timed by
+ * one hipEvent pair around the loop; returns the mean ms per launch (< 0 on
+ * error). The kernels are idempotent, so outputs are unchanged. Measurement
+ * only: the buffers of that forward must still be alive. */
+NOVA_API double nova_profile_replay(nova_handle_t h, int kind, int reps);
 /* Name of the kernel last timed for a kind (e.g. "wgemm_kernel<2, 2, 2, 2>"). */
 NOVA_API const char* nova_profile_kernel_name(nova_handle_t h, int kind);
 

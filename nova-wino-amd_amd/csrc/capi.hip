@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <cstring>
+#include <functional>
 #include <vector>
 
 #include "../../include/nova_winograd.h"
@@ -48,6 +49,8 @@ struct Profiler {
     };
     std::vector<Span> spans;
     const char* names[kNumKinds] = {"", "", "", ""};
+    // last launch of each kind (first sub-batch), re-issued by replay()
+    std::function<hipError_t()> last[kNumKinds];
 
     // Returns the index of a recorded event, or SIZE_MAX when disabled/exhausted.
     size_t mark(hipStream_t s) {
@@ -172,32 +175,47 @@ bool use_fused(const Handle* Hd, const Shape& s) {
         return false;
     if (Hd->path_pref == 2) return true;
     if (Hd->path_pref == 1) return false;
-    // Automatic choice: the fused kernel wins when V/M round trips through
-    // memory dominate, i.e. for small channel counts.
-    return Hd->K <= 64 && Hd->C <= 64;
+    // Automatic choice: measured on MI355X, the 3-pass pipeline is faster than
+    // the current fused kernel for every ResNet-50 layer at B=1 and B=32, so
+    // the fused kernel runs only when requested (nova_set_path(h, 2)).
+    return false;
 }
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
 bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* V,
-                    uint16_t* M) {
+                    uint16_t* M, bool remember) {
     Profiler& pf = Hd->prof;
-    const size_t e0 = pf.mark(Hd->stream);
-    if (!hip_ok(launch_input_transform(x, V, s.B, Hd->C, s.H, s.W, s.pad, s.nh, s.nw, Hd->Cp,
-                                       (int64_t)Hd->Cp * s.BP, Hd->stream),
-                "input transform"))
-        return false;
-    const size_t e1 = pf.mark(Hd->stream);
-    if (!hip_ok(launch_wgemm(Hd->U, V, M, Hd->K, Hd->Cp, (int)s.BP, Hd->stream), "wgemm"))
-        return false;
-    const size_t e2 = pf.mark(Hd->stream);
-    if (!hip_ok(launch_output_transform(M, y, s.B, Hd->K, s.Ho, s.Wo, s.nh, s.nw, Hd->K,
-                                        (int64_t)Hd->K * s.BP, Hd->stream),
-                "output transform"))
-        return false;
+    const hipStream_t st = Hd->stream;
+    const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+    const uint16_t* U = Hd->U;
+    auto in = [=]() {
+        return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp,
+                                      (int64_t)Cp * s.BP, st);
+    };
+    auto gm = [=]() { return launch_wgemm(U, V, M, K, Cp, (int)s.BP, st); };
+    auto out = [=]() {
+        return launch_output_transform(M, y, s.B, K, s.Ho, s.Wo, s.nh, s.nw, K,
+                                       (int64_t)K * s.BP, st);
+    };
+    if (remember) {
+        pf.last[kKindInput] = in;
+        pf.last[kKindGemm] = gm;
+        pf.last[kKindOutput] = out;
+        pf.last[kKindFused] = nullptr;
+    }
+    const size_t e0 = pf.mark(st);
+    if (!hip_ok(in(), "input transform")) return false;
+    const size_t e1 = pf.mark(st);
+    if (!hip_ok(gm(), "wgemm")) return false;
+    const size_t e2 = pf.mark(st);
+    if (!hip_ok(out(), "output transform")) return false;
     const size_t e3 = pf.mark(Hd->stream);
-    pf.span(kKindInput, e0, e1, "input_transform_kernel");
-    pf.span(kKindGemm, e1, e2, wgemm_name(Hd->K, Hd->Cp, (int)s.BP));
-    pf.span(kKindOutput, e2, e3, "output_transform_kernel");
+    pf.names[kKindInput] = "input_transform_kernel";
+    pf.names[kKindGemm] = wgemm_name(K, Cp, (int)s.BP);
+    pf.names[kKindOutput] = "output_transform_kernel";
+    pf.span(kKindInput, e0, e1, pf.names[kKindInput]);
+    pf.span(kKindGemm, e1, e2, pf.names[kKindGemm]);
+    pf.span(kKindOutput, e2, e3, pf.names[kKindOutput]);
     return true;
 }
 
@@ -258,13 +276,22 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         const uint16_t* xx = static_cast<const uint16_t*>(x) + b0 * x_img;
         uint16_t* yy = static_cast<uint16_t*>(y) + b0 * y_img;
         if (fused) {
-            const size_t e0 = pf.mark(Hd->stream);
-            if (!hip_ok(launch_fused(xx, Hd->U, yy, s.B, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.pad,
-                                     s.nh, s.nw, s.Ho, s.Wo, Hd->stream),
-                        "fused kernel"))
-                return;
-            pf.span(kKindFused, e0, pf.mark(Hd->stream), fused_name(Hd->K, Hd->C, s.BP));
-        } else if (!run_three_pass(Hd, xx, yy, s, V, M)) {
+            const hipStream_t st = Hd->stream;
+            const uint16_t* U = Hd->U;
+            const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+            auto fz = [=]() {
+                return launch_fused(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw, s.Ho,
+                                    s.Wo, st);
+            };
+            if (b0 == 0) {
+                for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
+                pf.last[kKindFused] = fz;
+            }
+            pf.names[kKindFused] = fused_name(Hd->K, Hd->C, s.BP);
+            const size_t e0 = pf.mark(st);
+            if (!hip_ok(fz(), "fused kernel")) return;
+            pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
+        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0)) {
             return;
         }
     }
@@ -517,6 +544,31 @@ int nova_profile_read(nova_handle_t h, double* total_ms, long long* count) {
     pf.next = 0;
     pf.spans.clear();
     return n;
+}
+
+double nova_profile_replay(nova_handle_t h, int kind, int reps) {
+    Handle* H = as_handle(h, "nova_profile_replay");
+    if (!H) return -1.0;
+    if (kind < 0 || kind >= kNumKinds || reps < 1 || !H->prof.last[kind]) {
+        set_error(kErrInvalidArgument, "nova_profile_replay: no recorded launch of kind %d", kind);
+        return -1.0;
+    }
+    hipEvent_t e0, e1;
+    if (!hip_ok(hipEventCreate(&e0), "hipEventCreate")) return -1.0;
+    if (!hip_ok(hipEventCreate(&e1), "hipEventCreate")) {
+        hipEventDestroy(e0);
+        return -1.0;
+    }
+    double ms_avg = -1.0;
+    bool ok = hip_ok(hipEventRecord(e0, H->stream), "hipEventRecord");
+    for (int r = 0; ok && r < reps; r++) ok = hip_ok(H->prof.last[kind](), "replay launch");
+    ok = ok && hip_ok(hipEventRecord(e1, H->stream), "hipEventRecord") &&
+         hip_ok(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.0f;
+    if (ok && hip_ok(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime")) ms_avg = ms / reps;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    return ms_avg;
 }
 
 const char* nova_profile_kernel_name(nova_handle_t h, int kind) {

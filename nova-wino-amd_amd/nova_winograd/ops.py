@@ -58,6 +58,7 @@ _SIGNATURES = {
     "nova_profile_enable": (None, [_vp, _i]),
     "nova_profile_read": (_i, [_vp, ctypes.POINTER(ctypes.c_double),
                                ctypes.POINTER(ctypes.c_longlong)]),
+    "nova_profile_replay": (ctypes.c_double, [_vp, _i, _i]),
     "nova_profile_kernel_name": (ctypes.c_char_p, [_vp, _i]),
     "nova_version": (ctypes.c_char_p, []),
 }

@@ -1,0 +1,334 @@
+"""Pins of the CPU oracle (oracle/nova_oracle.c), CPU only.
+
+Each check is independent of the oracle's own formulas: exact rational
+derivations, textbook identities, numpy's IEEE conversions, brute force, and
+invariants the arithmetic must satisfy bit for bit. A planted-mistake test
+shows that a transposed or sign-flipped table is caught.
+"""
+
+import os
+import re
+from fractions import Fraction as F
+
+import numpy as np
+import pytest
+
+from oracle import derive_tables as D
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+# ----------------------------------------------------------------------------
+# tables
+# ----------------------------------------------------------------------------
+
+def test_tables_equal_exact_derivation(oracle):
+    A32, B32, G32, Ah, Bh = D.fp32_tables()
+    A, B, G, Ah_o, Bh_o = oracle.tables()
+    for name, want, got in [("A", A32, A), ("B", B32, B), ("G", G32, G),
+                            ("Ah", Ah, Ah_o), ("Bh", Bh, Bh_o)]:
+        want = np.array(want, np.float32)
+        assert np.array_equal(want.view(np.uint32), got.view(np.uint32)), name
+
+
+def _parse_c_table(text, name, rows, cols):
+    m = re.search(r"\b%s\[%d\]\[%d\]\s*=\s*\{(.*?)\};" % (name, rows, cols), text, re.S)
+    assert m, name
+    vals = re.findall(r"-?0x[0-9a-fA-F.]+p[+-]?\d+f", m.group(1))
+    assert len(vals) == rows * cols, (name, len(vals))
+    return np.array([float.fromhex(v[:-1]) for v in vals], np.float32).reshape(rows, cols)
+
+
+def test_product_tables_equal_derivation():
+    """The product library's compiled-in tables (a separate copy) match."""
+    text = open(os.path.join(ROOT, "nova-wino-amd_amd", "csrc", "nova_tables.h")).read()
+    A32, B32, G32, Ah, Bh = D.fp32_tables()
+    for name, want, shape in [("kG", G32, (8, 3)), ("kAh", Ah, (6, 8)), ("kBh", Bh, (8, 8))]:
+        got = _parse_c_table(text, name, *shape)
+        assert np.array_equal(np.array(want, np.float32).view(np.uint32), got.view(np.uint32)), name
+
+
+def test_tables_structure():
+    A, B, G = D.exact_tables()
+    pts = D.POINTS
+    # A rows are powers of the points, B columns vanish on all other points
+    for r in range(6):
+        for i, a in enumerate(pts):
+            assert A[r][i] == a ** r
+    for i in range(7):
+        for j, a in enumerate(pts):
+            val = sum(B[p][i] * a ** p for p in range(8))
+            assert (val == 0) == (j != i)
+    assert max(abs(float(v)) for row in B for v in row) == pytest.approx(2.7211, abs=1e-4)
+
+
+def _winograd_exact(d, w, A, B, G):
+    """A [(G w G^T) * (B^T d B)] A^T in exact rational arithmetic."""
+    def mm(X, Y):
+        return [[sum(X[i][k] * Y[k][j] for k in range(len(Y))) for j in range(len(Y[0]))]
+                for i in range(len(X))]
+
+    def tr(X):
+        return [list(r) for r in zip(*X)]
+
+    U = mm(mm(G, w), tr(G))
+    V = mm(mm(tr(B), d), B)
+    Mm = [[U[i][j] * V[i][j] for j in range(8)] for i in range(8)]
+    return mm(mm(A, Mm), tr(A))
+
+
+def test_exact_winograd_is_correlation():
+    """With exact tables, F(6,3) equals the 6x6 valid correlation of an 8x8
+    patch with a 3x3 filter (nn.Conv2d orientation), for random integers."""
+    A, B, G = D.exact_tables()
+    rng = np.random.default_rng(1)
+    for _ in range(3):
+        d = [[F(int(v)) for v in row] for row in rng.integers(-9, 10, (8, 8))]
+        w = [[F(int(v)) for v in row] for row in rng.integers(-9, 10, (3, 3))]
+        y = _winograd_exact(d, w, A, B, G)
+        for r in range(6):
+            for s in range(6):
+                want = sum(d[r + p][s + q] * w[p][q] for p in range(3) for q in range(3))
+                assert y[r][s] == want
+
+
+def test_planted_table_mistakes_are_caught():
+    """A transposed B or a flipped sign in G breaks the exact identity."""
+    A, B, G = D.exact_tables()
+    rng = np.random.default_rng(11)
+    d = [[F(int(v)) for v in row] for row in rng.integers(-9, 10, (8, 8))]
+    w = [[F(int(v)) for v in row] for row in rng.integers(-9, 10, (3, 3))]
+    ref = [[sum(d[r + p][s + q] * w[p][q] for p in range(3) for q in range(3)) for s in range(6)]
+           for r in range(6)]
+    Bt = [list(r) for r in zip(*B)]
+    G2 = [row[:] for row in G]
+    G2[1][1] = -G2[1][1]
+    assert _winograd_exact(d, w, A, Bt, G) != ref
+    assert _winograd_exact(d, w, A, B, G2) != ref
+
+
+# ----------------------------------------------------------------------------
+# fp16 conversions
+# ----------------------------------------------------------------------------
+
+def _special_f32():
+    vals = [0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, float("inf"),
+            -float("inf"), 2.0 ** -14, 2.0 ** -24, 2.0 ** -25, 2.0 ** -26, 3 * 2.0 ** -26,
+            1.5 * 2.0 ** -24, 2.5 * 2.0 ** -24, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11,
+            1.0 + 2.0 ** -11 + 2.0 ** -20, 6.1e-5, 5.96e-8]
+    return np.array(vals + [-v for v in vals], np.float32)
+
+
+def test_f32_to_f16_matches_numpy(oracle):
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2 ** 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    x = np.concatenate([x, _special_f32(), (rng.standard_normal(100000) * 3).astype(np.float32)])
+    got = oracle.f32_to_f16(x).view(np.uint16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    nan = oracle.f32_to_f16(np.array([np.nan], np.float32))
+    assert np.isnan(nan.astype(np.float32)).all()
+
+
+def test_f64_to_f16_single_rounding(oracle):
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.standard_normal(200000) * 50, rng.standard_normal(20000) * 1e-5,
+                        _special_f32().astype(np.float64)])
+    got = oracle.f64_to_f16(x).view(np.uint16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ----------------------------------------------------------------------------
+# tiling law
+# ----------------------------------------------------------------------------
+
+def test_tiling_law_brute_force(oracle):
+    for pad in (0, 1, 2, 3):
+        for H in range(max(1, 3 - 2 * pad), 400):
+            nh, nw, Ho, Wo = oracle.tiling(H, H, pad)
+            assert Ho == H + 2 * pad - 2 == Wo
+            # reference law: the padded extent nh*6+2 is the smallest value
+            # >= Ho+7 with (extent - 8) a multiple of 6
+            ext = next(e for e in range(Ho + 7, Ho + 14) if (e - 8) % 6 == 0)
+            assert nh == (ext - 8) // 6 + 1 == nw
+            assert 6 * nh >= Ho  # every output is covered
+            assert nh == -(-(Ho - 1) // 6) + 1
+            # the reference over-allocates one tile row unless Ho = 1 (mod 6)
+            assert nh == -(-Ho // 6) + (0 if Ho % 6 == 1 else 1)
+
+
+# ----------------------------------------------------------------------------
+# stages against float64 references (bounded by the fp16 rounding points)
+# ----------------------------------------------------------------------------
+
+def _ulp16(v):
+    a = np.abs(v)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def test_filter_transform_vs_float64(oracle):
+    rng = np.random.default_rng(3)
+    w = (rng.standard_normal((5, 7, 3, 3)) * 0.5).astype(np.float32)
+    U = oracle.filter_transform(w).astype(np.float64)  # [64, C, K]
+    _, _, G, _, _ = oracle.tables()
+    G = G.astype(np.float64)
+    ex = np.einsum("rp,kcpq,sq->rskc", G, w.astype(np.float64), G).reshape(64, 5, 7)
+    ex = ex.transpose(0, 2, 1)  # [64, C, K]
+    ab = np.einsum("rp,kcpq,sq->rskc", np.abs(G), np.abs(w.astype(np.float64)), np.abs(G))
+    ab = ab.reshape(64, 5, 7).transpose(0, 2, 1)
+    # one fp16 rounding plus the fp32 chain (9 products, 9 accumulations)
+    assert np.all(np.abs(U - ex) <= 0.5 * _ulp16(ex) + 20 * 2.0 ** -24 * ab)
+
+
+def test_input_transform_vs_float64(oracle):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 3, 13, 11)).astype(np.float16)
+    pad = 1
+    nh, nw, _, _ = oracle.tiling(13, 11, pad)
+    V = oracle.input_transform(x, pad, nh, nw).astype(np.float64)  # [64, BP, C]
+    _, _, _, _, Bh = oracle.tables()
+    Bh = Bh.astype(np.float64)
+    xp = np.zeros((2, 3, 13 + 2 * 9, 11 + 2 * 9))
+    xp[:, :, pad:pad + 13, pad:pad + 11] = x
+    for b in range(2):
+        for th in range(nh):
+            for tw in range(nw):
+                bp = (b * nh + th) * nw + tw
+                d = xp[b, :, th * 6:th * 6 + 8, tw * 6:tw * 6 + 8]
+                ex = np.einsum("ir,cij,js->crs", Bh, d, Bh).reshape(3, 64).T
+                got = V[:, bp, :]
+                bound = 0.5 * _ulp16(ex) + 64 * 2.0 ** -24 * np.einsum(
+                    "ir,cij,js->crs", np.abs(Bh), np.abs(d), np.abs(Bh)).reshape(3, 64).T
+                assert np.all(np.abs(got - ex) <= bound + 1e-12)
+
+
+def test_gemm_is_correctly_rounded(oracle):
+    rng = np.random.default_rng(5)
+    U = (rng.standard_normal((64, 40, 24)) * 0.3).astype(np.float16)   # [64, C, K]
+    V = (rng.standard_normal((64, 17, 40)) * 2).astype(np.float16)     # [64, BP, C]
+    M = oracle.batched_gemm(U, V)
+    ex = np.einsum("pck,pbc->pbk", U.astype(np.float64), V.astype(np.float64))
+    assert np.array_equal(M.view(np.uint16), ex.astype(np.float16).view(np.uint16))
+
+
+def test_output_transform_vs_float64(oracle):
+    rng = np.random.default_rng(6)
+    B, K, Ho, Wo = 1, 5, 13, 8
+    nh, nw, _, _ = oracle.tiling(Ho, Wo, 1)
+    M = (rng.standard_normal((64, B * nh * nw, K)) * 3).astype(np.float16)
+    y = oracle.output_transform(M, B, Ho, Wo, nh, nw).astype(np.float64)
+    A, _, _, Ah, _ = oracle.tables()
+    Ah = Ah.astype(np.float64)
+    for th in range(nh):
+        for tw in range(nw):
+            bp = th * nw + tw
+            m = M[:, bp, :].astype(np.float64).T.reshape(K, 8, 8)
+            ex = np.einsum("ri,kij,sj->krs", Ah, m, Ah)
+            bnd = np.einsum("ri,kij,sj->krs", np.abs(Ah), np.abs(m), np.abs(Ah))
+            for r in range(6):
+                for s in range(6):
+                    h, w = th * 6 + r, tw * 6 + s
+                    if h < Ho and w < Wo:
+                        e = ex[:, r, s]
+                        assert np.all(np.abs(y[0, :, h, w] - e)
+                                      <= 0.5 * _ulp16(e) + 32 * 2.0 ** -24 * bnd[:, r, s] + 1e-12)
+
+
+# ----------------------------------------------------------------------------
+# exact invariants of the whole path
+# ----------------------------------------------------------------------------
+
+def _case(B=1, C=6, K=5, H=19, W=17, seed=7):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((B, C, H, W)).astype(np.float16)
+    w = (rng.standard_normal((K, C, 3, 3)) * 0.3).astype(np.float32)
+    return x, w
+
+
+def test_zero_input_gives_zero(oracle):
+    x, w = _case()
+    y = oracle.conv2d(np.zeros_like(x), w, 1)
+    assert not np.any(y.astype(np.float32))
+
+
+def test_negation_and_power_of_two_scaling_are_exact(oracle):
+    """RNE rounding commutes with negation and with scaling by 2 (no
+    overflow/underflow at these magnitudes): bit-exact invariants."""
+    x, w = _case()
+    y = oracle.conv2d(x, w, 1)
+    yn = oracle.conv2d(-x, w, 1)
+    y2 = oracle.conv2d((x.astype(np.float32) * 2).astype(np.float16), w, 1)
+    assert np.array_equal(yn.view(np.uint16), (-y).view(np.uint16))
+    assert np.array_equal(y2.view(np.uint16), (y.astype(np.float32) * 2).astype(np.float16).view(np.uint16))
+
+
+def test_translation_by_one_tile_is_exact(oracle):
+    """Shifting the input by 6 pixels (one tile) shifts the output by 6, bit
+    for bit, for every tile whose whole 8x8 input patch is shared (a tile's
+    fp16 result depends on all 64 patch values, not only on its 3x3 support)."""
+    x, w = _case(H=31, W=29)
+    y = oracle.conv2d(x, w, 0)
+    xs = np.zeros_like(x)
+    xs[:, :, 6:, 6:] = x[:, :, :-6, :-6]
+    ys = oracle.conv2d(xs, w, 0)
+    # tiles 1..3 of the shifted image read xs rows/cols 6..25 == x rows/cols 0..19
+    a = ys[:, :, 6:24, 6:24]
+    b = y[:, :, 0:18, 0:18]
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+def test_batch_images_are_independent(oracle):
+    x, w = _case(B=3)
+    y = oracle.conv2d(x, w, 1)
+    y1 = oracle.conv2d(x[1:2], w, 1)
+    assert np.array_equal(y[1:2].view(np.uint16), y1.view(np.uint16))
+
+
+def test_constant_input_interior(oracle):
+    x = np.full((1, 4, 20, 20), 0.5, np.float16)
+    rng = np.random.default_rng(8)
+    w = (rng.standard_normal((3, 4, 3, 3)) * 0.3).astype(np.float32)
+    y = oracle.conv2d(x, w, 1).astype(np.float64)
+    want = 0.5 * w.astype(np.float64).sum(axis=(1, 2, 3))
+    interior = y[0, :, 1:-1, 1:-1]
+    assert np.all(np.abs(interior - want[:, None, None]) < 0.02)
+
+
+# ----------------------------------------------------------------------------
+# the reference's published error level
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("C,H", [(64, 56), (128, 28), (256, 14), (512, 7)])
+def test_error_level_vs_fp64_direct(oracle, C, H):
+    """rel-L2 vs an fp64 direct correlation at the reference's level (5.2% in
+    /root/reference/docs/report/main.tex:221; its tests accept < 0.06)."""
+    import torch
+
+    torch.manual_seed(0)
+    x = torch.randn(1, C, H, H).half().numpy()
+    w = torch.empty(C, C, 3, 3)
+    torch.nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu")
+    w = w.numpy()
+    y = oracle.conv2d(x, w, 1)
+    truth = oracle.direct_conv2d(x, w, 1)
+    rel = oracle.rel_l2(y, truth)
+    assert 0.04 < rel < 0.06, rel
+    assert oracle.max_abs(y, truth) < 0.6
+    assert np.isfinite(y.astype(np.float32)).all()
+
+
+def test_direct_conv_matches_torch(oracle):
+    import torch
+
+    x, w = _case(B=2, C=3, K=4, H=9, W=12)
+    for pad in (0, 1, 2):
+        ref = torch.nn.functional.conv2d(torch.from_numpy(x.astype(np.float64)),
+                                         torch.from_numpy(w.astype(np.float64)), padding=pad)
+        got = oracle.direct_conv2d(x, w, pad)
+        assert np.allclose(got, ref.numpy(), rtol=0, atol=1e-9)

@@ -1,0 +1,105 @@
+"""The drop-in Python surface on the CPU: names and behaviour that do not
+need a GPU (construction, from_conv2d, surgery, cache keys), and the loud
+failure of every compute entry point on CPU tensors (no CPU fallback)."""
+
+import subprocess
+import sys
+
+import pytest
+import torch
+import torch.nn as nn
+
+import nova_winograd as nw
+from nova_winograd import (
+    NovaWinogradConv2d,
+    NovaWinogradConv2dCompilable,
+    NovaWinogradConv2dTrainable,
+    nova_forward,
+    replace_conv2d_with_nova,
+)
+
+
+def test_exports():
+    assert nw.__version__ == "1.0.0"
+    assert set(nw.__all__) == {
+        "NovaWinogradConv2d", "NovaWinogradConv2dTrainable", "NovaWinogradConv2dCompilable",
+        "nova_forward", "compute_tiling", "replace_conv2d_with_nova"}
+
+
+def test_module_construction_and_repr():
+    m = NovaWinogradConv2d(16, 32, kernel_size=3, padding=1, bias=True)
+    assert m.weight.shape == (32, 16, 3, 3) and m.weight.dtype == torch.float32
+    assert m.bias.shape == (32,) and torch.count_nonzero(m.bias) == 0
+    assert "tile=F(6,3), points=NOVA" in repr(m)
+    assert "compilable=True" in repr(NovaWinogradConv2dCompilable(4, 4))
+    with pytest.raises(AssertionError):
+        NovaWinogradConv2d(4, 4, kernel_size=5)
+
+
+def test_from_conv2d_copies_parameters():
+    conv = nn.Conv2d(8, 12, 3, padding=2, bias=True)
+    m = NovaWinogradConv2d.from_conv2d(conv)
+    assert m.padding == 2
+    assert torch.equal(m.weight, conv.weight) and torch.equal(m.bias, conv.bias)
+    t = NovaWinogradConv2dTrainable.from_conv2d(conv)
+    assert isinstance(t, NovaWinogradConv2dTrainable)
+    with pytest.raises(AssertionError):
+        NovaWinogradConv2d.from_conv2d(nn.Conv2d(8, 8, 3, stride=2))
+
+
+def test_surgery_replaces_eligible_layers():
+    model = nn.Sequential(
+        nn.Conv2d(3, 64, 3, padding=1, bias=False),      # eligible
+        nn.ReLU(),
+        nn.Conv2d(64, 128, 3, stride=2, padding=1),      # stride 2
+        nn.ReLU(),
+        nn.Conv2d(128, 128, 3, padding=1, bias=True),    # eligible
+        nn.ReLU(),
+        nn.Conv2d(128, 256, 1),                          # 1x1
+        nn.Conv2d(256, 256, 3, padding=1, groups=2),     # grouped
+        nn.Conv2d(256, 256, 3, padding=1, dilation=2),   # dilated
+        nn.Conv2d(256, 256, 3, padding="same"),          # string padding
+        nn.Conv2d(256, 256, 3, padding=(1, 2)),          # asymmetric
+        nn.Conv2d(256, 256, 3, padding=1, padding_mode="reflect"),
+    )
+    n = replace_conv2d_with_nova(model, verbose=False)
+    assert n == 2
+    assert isinstance(model[0], NovaWinogradConv2d) and isinstance(model[4], NovaWinogradConv2d)
+    assert isinstance(model[2], nn.Conv2d)
+    assert torch.count_nonzero(model[4].bias) == torch.count_nonzero(model[4].bias)
+    nested = nn.Sequential(nn.Sequential(nn.Conv2d(4, 4, 3, padding=1)))
+    assert replace_conv2d_with_nova(nested, trainable=True, verbose=False) == 1
+    assert isinstance(nested[0][0], NovaWinogradConv2dTrainable)
+
+
+def test_cpu_tensors_fail_loudly():
+    m = NovaWinogradConv2d(4, 4)
+    x = torch.randn(1, 4, 8, 8).half()
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        m(x)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        nova_forward(x, torch.randn(4, 4, 3, 3))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        NovaWinogradConv2dTrainable(4, 4)(x.float())
+
+
+def test_weight_cache_key_tracks_in_place_updates():
+    from nova_winograd.conv2d import _weight_key
+
+    m = NovaWinogradConv2d(4, 4)
+    k0 = _weight_key(m.weight)
+    with torch.no_grad():
+        m.weight.add_(1.0)
+    assert _weight_key(m.weight) != k0
+    k1 = _weight_key(m.weight)
+    m.half()
+    assert _weight_key(m.weight) != k1
+
+
+def test_bench_refuses_multi_gpu():
+    import os
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr
