@@ -135,7 +135,7 @@ def pmc_workload(runs, reps, torch):
     n = COPY_MIB * (1 << 20) // 2
     src = torch.ones(n, dtype=torch.float16, device="cuda")
     dst = torch.empty_like(src)
-    dst.copy_(src)
+    torch.neg(src, out=dst)  # one elementwise kernel: reads and writes COPY_MIB each
     torch.cuda.synchronize()
     for r in runs:
         for _ in range(reps):
@@ -143,43 +143,82 @@ def pmc_workload(runs, reps, torch):
     torch.cuda.synchronize()
 
 
-def traffic_from(fetch_dir, write_dir, out_path, kernel_name):
-    """HBM bytes per launch of `kernel_name` from two rocprofv3 --pmc runs of
-    `bench.py --pmc-mode` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
-    scaled by the same counter's reading for the known-size copy kernel."""
+NOVA_KERNELS = ["input_transform_kernel", "output_transform_kernel",
+                "wgemm_kernel<1, 1, 4, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2>",
+                "wgemm_lds_kernel<128, 128, 2, 2>", "fused_block_kernel", "fused_kernel<1>",
+                "fused_kernel<2>", "fused_kernel<4>"]
+
+
+def _name_keys(name):
+    """The kernel's name as it appears demangled and Itanium-mangled (int
+    template arguments only), for matching rocprofv3 records."""
+    if "<" not in name:
+        return [name]
+    base, args = name.split("<", 1)
+    args = [a.strip() for a in args.rstrip(">").split(",")]
+    return [name, base + "I" + "".join(f"Li{a}E" for a in args) + "E"]
+
+
+def traffic_from(fetch_dir, write_dir, out_path):
+    """HBM bytes per launch of each library kernel from two rocprofv3 --pmc runs
+    of `bench.py --pmc-mode` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
+    each scaled by the same counter's reading for the known-size copy kernel.
+    The figure kept per kernel is the mean over the layers it ran on, the same
+    averaging as the bench line's avg_launch_us."""
     import glob
     import sqlite3
 
     def read(d, counter):
-        db = sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True))[-1]
-        con = sqlite3.connect(db)
-        rows = con.execute("select kernel_name, grid_size, avg(value), count(*) from "
-                           "counters_collection where counter_name = ? group by kernel_name, "
-                           "grid_size", (counter,)).fetchall()
-        copy = [r for r in rows if "copy" in r[0].lower() and r[1] >= COPY_MIB * (1 << 20) // 16]
-        kern = [r for r in rows if kernel_name in r[0]]
-        if not copy or not kern:
-            raise SystemExit(f"{counter}: copy kernel or {kernel_name} not found in {db}")
-        copy_kib = max(copy, key=lambda r: r[1])[2]
-        mean_kib = sum(r[2] for r in kern) / len(kern)  # one launch per layer
+        dbs = sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True))
+        if not dbs:
+            raise SystemExit(f"no rocprofv3 database under {d}")
+        con = sqlite3.connect(dbs[-1])
+        tabs = [r[0] for r in con.execute("select name from sqlite_master where type in "
+                                          "('table','view')")]
+        rows = None
+        for t in tabs:
+            cols = [c[1] for c in con.execute(f"pragma table_info('{t}')")]
+            if {"kernel_name", "counter_name", "value"} <= set(cols):
+                gcol = "grid_size" if "grid_size" in cols else "grid_size_x"
+                rows = con.execute(f"select kernel_name, {gcol}, avg(value), count(*) from '{t}' "
+                                   f"where counter_name = ? group by kernel_name, {gcol}",
+                                   (counter,)).fetchall()
+                break
+        if rows is None:
+            raise SystemExit(f"no counter table in {dbs[-1]}: {tabs}")
+        copy = [r for r in rows if "copy" in r[0].lower() or "elementwise" in r[0].lower()]
+        copy = [r for r in copy if r[2] > COPY_MIB * 1024 * 0.5]
+        if not copy:
+            raise SystemExit(f"{counter}: calibration copy not found in {dbs[-1]}")
+        copy_kib = min(copy, key=lambda r: abs(r[2] - COPY_MIB * 1024))[2]
         factor = COPY_MIB * 1024.0 / copy_kib
-        return mean_kib * 1024.0 * factor, factor, [(r[1], r[2]) for r in kern]
+        per = {}
+        for name in NOVA_KERNELS:
+            kern = [r for r in rows if any(k in r[0] for k in _name_keys(name))]
+            if kern:
+                per[name] = (sum(r[2] for r in kern) / len(kern) * 1024.0 * factor,
+                             [(r[1], round(r[2], 1)) for r in kern])
+        return per, factor, copy_kib
 
-    fetch, ff, fk = read(fetch_dir, "FETCH_SIZE")
-    write, wf, wk = read(write_dir, "WRITE_SIZE")
-    rec = {"kernel": kernel_name, "hbm_bytes_per_launch": round(fetch + write),
-           "fetch_bytes_per_launch": round(fetch), "write_bytes_per_launch": round(write),
-           "fetch_scale": round(ff, 4), "write_scale": round(wf, 4),
-           "copy_calibration_bytes": COPY_MIB * (1 << 20),
-           "per_grid_kib": {"fetch": fk, "write": wk}}
-    data = {"kernels": []}
-    if os.path.exists(out_path):
-        with open(out_path) as f:
-            data = json.load(f)
-    data["kernels"] = [k for k in data["kernels"] if k.get("kernel") != kernel_name] + [rec]
+    fetch, ff, fcopy = read(fetch_dir, "FETCH_SIZE")
+    write, wf, wcopy = read(write_dir, "WRITE_SIZE")
+    data = {"method": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (separate runs) of "
+                      "bench.py --pmc-mode; each scaled by copy_bytes / counter reading of a "
+                      f"{COPY_MIB} MiB device copy in the same run",
+            "copy_bytes": COPY_MIB * (1 << 20), "fetch_copy_kib": round(fcopy, 1),
+            "write_copy_kib": round(wcopy, 1), "fetch_scale": round(ff, 4),
+            "write_scale": round(wf, 4), "kernels": []}
+    for name in NOVA_KERNELS:
+        if name in fetch and name in write:
+            data["kernels"].append({
+                "kernel": name,
+                "hbm_bytes_per_launch": round(fetch[name][0] + write[name][0]),
+                "fetch_bytes_per_launch": round(fetch[name][0]),
+                "write_bytes_per_launch": round(write[name][0]),
+                "fetch_kib_by_grid": fetch[name][1], "write_kib_by_grid": write[name][1]})
     with open(out_path, "w") as f:
         json.dump(data, f, indent=1)
-    print(json.dumps(rec))
+    print(json.dumps(data))
 
 
 def cpu_baseline(layers_spec, budget_s, threads):
@@ -262,12 +301,11 @@ def main():
                     help="short run for rocprofv3 --pmc passes (copy calibration + forwards)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two --pmc-mode profiles into profiles/traffic.json and exit")
-    ap.add_argument("--traffic-kernel", default="input_transform_kernel")
     args = ap.parse_args()
 
     if args.traffic_from:
         traffic_from(args.traffic_from[0], args.traffic_from[1],
-                     os.path.join(ROOT, "profiles", "traffic.json"), args.traffic_kernel)
+                     os.path.join(ROOT, "profiles", "traffic.json"))
         return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -369,7 +407,7 @@ def main():
         for r in runs:
             mod, mio, x = r["mod"], r["mio"], r["x"]
             r["nova_ms"] = time_region(lambda: mod(x), args.layer_reps, torch)
-            r["path"] = {1: "3-pass", 2: "fused"}.get(lib.nova_get_last_path(mod._handle.h), "?")
+            r["path"] = {1: "3-pass", 2: "fused_rows", 3: "fused_block"}.get(lib.nova_get_last_path(mod._handle.h), "?")
             if not args.no_miopen:
                 r["miopen_ms"] = time_region(lambda: mio(x), args.layer_reps, torch)
             if not args.no_graph:

@@ -111,10 +111,13 @@ NOVA_API const char* nova_get_last_error_message(void);
 /* Stream for the handle's subsequent work (a hipStream_t; NULL = null stream). */
 NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
 
-/* Path selection: 0 = automatic (default), 1 = force 3-pass, 2 = force fused
- * (falls back to 3-pass with an error if the shape is unsupported). */
+/* Path selection: 0 = automatic (default), 1 = force 3-pass, 2 = force the
+ * fused kernel split by position row (small batches), 3 = force the fused
+ * tile-block kernel (few channels, batch > 1). A forced fused path outside its
+ * envelope runs 3-pass and reports an error. */
 NOVA_API void nova_set_path(nova_handle_t h, int path);
-/* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused. */
+/* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused
+ * (position rows), 3 = fused (tile blocks). */
 NOVA_API int nova_get_last_path(nova_handle_t h);
 
 /* Internal workspace bytes a forward of this shape needs on this handle. */

@@ -70,10 +70,14 @@ struct Handle {
     int K = 0, C = 0, Cp = 0;
     uint16_t* U = nullptr;
     size_t U_cap = 0;  // bytes
+    uint16_t* Uf = nullptr;  // U in MFMA fragment order (fused kernels)
+    size_t Uf_cap = 0;       // bytes
     void* ws = nullptr;
     size_t ws_cap = 0;  // bytes
+    unsigned* cnt = nullptr;  // fused-kernel arrival counters, zero between launches
+    size_t cnt_cap = 0;       // counters
     hipStream_t stream = nullptr;
-    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused
+    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block
     int last_path = 0;
     bool ready = false;
     Profiler prof;
@@ -122,6 +126,24 @@ bool ensure_ws(Handle* H, size_t bytes) {
     return true;
 }
 
+// Counters of the fused kernel: zeroed once when (re)allocated; each launch
+// returns every counter it uses to zero.
+bool ensure_cnt(Handle* H, size_t count) {
+    if (count <= H->cnt_cap) return true;
+    if (H->cnt) {
+        if (!hip_ok(hipFree(H->cnt), "hipFree(counters)")) return false;
+        H->cnt = nullptr;
+        H->cnt_cap = 0;
+    }
+    const size_t want = count + count / 4 + 64;
+    if (!hip_ok(hipMalloc(&H->cnt, want * sizeof(unsigned)), "hipMalloc(counters)")) return false;
+    if (!hip_ok(hipMemsetAsync(H->cnt, 0, want * sizeof(unsigned), H->stream),
+                "hipMemsetAsync(counters)"))
+        return false;
+    H->cnt_cap = want;
+    return true;
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct Shape {
@@ -166,19 +188,49 @@ int64_t batch_chunk(const Handle* Hd, const Shape& s) {
     return ((int64_t)1 << 31) / 2 / per_img;  // keep a 2x margin under INT_MAX
 }
 
-bool use_fused(const Handle* Hd, const Shape& s) {
-    if (!fused_supported(Hd->K, Hd->C)) return false;
-    // per launch the batch is split so that x and y stay below 1 GB
-    const int64_t Bc = std::min<int64_t>(s.B, std::max<int64_t>(1, batch_chunk(Hd, s)));
+// Sub-batch size of a forward (every buffer a kernel addresses < 1 GB).
+int64_t sub_batch(const Handle* Hd, const Shape& s) {
+    return std::min<int64_t>(s.B, std::max<int64_t>(1, batch_chunk(Hd, s)));
+}
+
+bool fused_plan_for(const Handle* Hd, const Shape& s, FusedPlan* p) {
+    const int64_t Bc = sub_batch(Hd, s);
+    if (s.pad > 16) return false;
     if (!fused_fits(Bc * Hd->C * s.H * s.W, (int64_t)64 * Hd->K * Hd->Cp,
                     Bc * Hd->K * s.Ho * s.Wo))
         return false;
-    if (Hd->path_pref == 2) return true;
-    if (Hd->path_pref == 1) return false;
-    // Automatic choice: measured on MI355X, the 3-pass pipeline is faster than
-    // the current fused kernel for every ResNet-50 layer at B=1 and B=32, so
-    // the fused kernel runs only when requested (nova_set_path(h, 2)).
-    return false;
+    return fused_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.nh, s.nw, p);
+}
+
+bool fused_block_plan_for(const Handle* Hd, const Shape& s, FusedBlockPlan* p) {
+    const int64_t Bc = sub_batch(Hd, s);
+    if (!fused_fits(Bc * Hd->C * s.H * s.W, u_frag_elems(Hd->K, Hd->Cp),
+                    Bc * Hd->K * s.Ho * s.Wo))
+        return false;
+    return fused_block_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.nh, s.nw, p);
+}
+
+// Pipeline for a forward: 1 three-pass, 2 fused (position-row split), 3 fused
+// (tile block). A requested fused variant outside its envelope falls back to
+// the three-pass pipeline.
+int choose_path(const Handle* Hd, const Shape& s) {
+    if (Hd->path_pref == 1) return 1;
+    if (Hd->path_pref == 2) {
+        FusedPlan p;
+        return fused_plan_for(Hd, s, &p) ? 2 : 1;
+    }
+    if (Hd->path_pref == 3) {
+        FusedBlockPlan p;
+        return fused_block_plan_for(Hd, s, &p) ? 3 : 1;
+    }
+    // Automatic choice, from MI355X measurements: the tile-block fused kernel
+    // wins for layers with at most 64 input and output channels once there
+    // are enough 16-tile runs to occupy the chip (ResNet-50 conv2_x at B=32:
+    // 32.6 us vs 41.3 us three-pass); everything else runs three-pass.
+    FusedBlockPlan bp;
+    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp) && bp.grid >= 128)
+        return 3;
+    return 1;
 }
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
@@ -236,11 +288,12 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         set_error(kErrInvalidArgument, "%s: a single image of this shape exceeds 1 GB buffers", fn);
         return;
     }
-    const bool fused = use_fused(Hd, s_all);
-    if (!fused && Hd->path_pref == 2) {
+    const int path = choose_path(Hd, s_all);
+    const bool fused = path != 1;
+    if (path == 1 && Hd->path_pref >= 2) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
-    Hd->last_path = fused ? 2 : 1;
+    Hd->last_path = path;
 
     // workspace for the largest sub-batch
     const int64_t Bc = std::min<int64_t>(chunk, s_all.B);
@@ -275,19 +328,49 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         s.BP = (int64_t)s.B * s.nh * s.nw;
         const uint16_t* xx = static_cast<const uint16_t*>(x) + b0 * x_img;
         uint16_t* yy = static_cast<uint16_t*>(y) + b0 * y_img;
-        if (fused) {
+        if (path == 3) {
             const hipStream_t st = Hd->stream;
-            const uint16_t* U = Hd->U;
+            const uint16_t* U = Hd->Uf;
             const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+            FusedBlockPlan bp;
+            if (!fused_block_plan((int)s.B, C, K, Cp, s.H, s.W, s.nh, s.nw, &bp)) {
+                set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
+                return;
+            }
             auto fz = [=]() {
-                return launch_fused(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw, s.Ho,
-                                    s.Wo, st);
+                return launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
+                                          s.Ho, s.Wo, bp, st);
             };
             if (b0 == 0) {
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
                 pf.last[kKindFused] = fz;
             }
-            pf.names[kKindFused] = fused_name(Hd->K, Hd->C, s.BP);
+            pf.names[kKindFused] = "fused_block_kernel";
+            const size_t e0 = pf.mark(st);
+            if (!hip_ok(fz(), "fused block kernel")) return;
+            pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
+        } else if (path == 2) {
+            const hipStream_t st = Hd->stream;
+            const uint16_t* U = Hd->U;
+            const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+            FusedPlan fp;
+            if (!fused_plan((int)s.B, C, K, Cp, s.H, s.W, s.nh, s.nw, &fp)) {
+                set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
+                return;
+            }
+            if (!ensure_ws(Hd, (size_t)fp.ms_bytes) || !ensure_cnt(Hd, (size_t)fp.cnt_count))
+                return;
+            uint16_t* Ms = static_cast<uint16_t*>(Hd->ws);
+            unsigned* cnt = Hd->cnt;
+            auto fz = [=]() {
+                return launch_fused(xx, U, yy, Ms, cnt, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh,
+                                    s.nw, s.Ho, s.Wo, fp, st);
+            };
+            if (b0 == 0) {
+                for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
+                pf.last[kKindFused] = fz;
+            }
+            pf.names[kKindFused] = fused_name(fp);
             const size_t e0 = pf.mark(st);
             if (!hip_ok(fz(), "fused kernel")) return;
             pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
@@ -315,8 +398,10 @@ void nova_destroy(nova_handle_t h) {
     Handle* H = as_handle(h, "nova_destroy");
     if (!H) return;
     if (H->U) hip_ok(hipFree(H->U), "hipFree(U)");
+    if (H->Uf) hip_ok(hipFree(H->Uf), "hipFree(Uf)");
     if (H->ws) hip_ok(hipFree(H->ws), "hipFree(workspace)");
-    for (hipEvent_t e : H->prof.pool) hipEventDestroy(e);
+    if (H->cnt) hip_ok(hipFree(H->cnt), "hipFree(counters)");
+    for (hipEvent_t e : H->prof.pool) (void)hipEventDestroy(e);
     H->magic = 0;
     delete H;
 }
@@ -343,12 +428,26 @@ void nova_set_weights(nova_handle_t h, const void* d_weight, int K, int C) {
         }
         H->U_cap = need;
     }
+    const size_t need_f = (size_t)u_frag_elems(K, Cp) * sizeof(uint16_t);
+    if (need_f > H->Uf_cap) {
+        if (H->Uf) {
+            if (!hip_ok(hipFree(H->Uf), "hipFree(Uf)")) return;
+            H->Uf = nullptr;
+            H->Uf_cap = 0;
+        }
+        if (!hip_ok(hipMalloc(&H->Uf, need_f), "hipMalloc(Uf)")) {
+            H->ready = false;
+            return;
+        }
+        H->Uf_cap = need_f;
+    }
     H->K = K;
     H->C = C;
     H->Cp = Cp;
     H->ready = hip_ok(launch_filter_transform_gemm(static_cast<const float*>(d_weight), H->U, K,
                                                    C, Cp, H->stream),
-                      "filter transform");
+                      "filter transform") &&
+               hip_ok(launch_u_frag(H->U, H->Uf, K, Cp, H->stream), "filter fragment order");
 }
 
 void nova_forward(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
@@ -482,8 +581,8 @@ void nova_set_stream(nova_handle_t h, void* stream) {
 void nova_set_path(nova_handle_t h, int path) {
     Handle* H = as_handle(h, "nova_set_path");
     if (!H) return;
-    if (path < 0 || path > 2) {
-        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1 or 2");
+    if (path < 0 || path > 3) {
+        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2 or 3");
         return;
     }
     H->path_pref = path;
@@ -499,7 +598,7 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     if (!Hd) return -1;
     Shape s;
     if (!make_shape(Hd, batch, H, W, pad, &s, "nova_workspace_bytes")) return -1;
-    if (Hd->ready && use_fused(Hd, s)) return 0;
+    if (Hd->ready && choose_path(Hd, s) != 1) return 0;
     const int64_t chunk = std::max<int64_t>(1, batch_chunk(Hd, s));
     const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;
     return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * BPc * 2);
@@ -556,7 +655,7 @@ double nova_profile_replay(nova_handle_t h, int kind, int reps) {
     hipEvent_t e0, e1;
     if (!hip_ok(hipEventCreate(&e0), "hipEventCreate")) return -1.0;
     if (!hip_ok(hipEventCreate(&e1), "hipEventCreate")) {
-        hipEventDestroy(e0);
+        (void)hipEventDestroy(e0);
         return -1.0;
     }
     double ms_avg = -1.0;
@@ -566,8 +665,8 @@ double nova_profile_replay(nova_handle_t h, int kind, int reps) {
          hip_ok(hipEventSynchronize(e1), "hipEventSynchronize");
     float ms = 0.0f;
     if (ok && hip_ok(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime")) ms_avg = ms / reps;
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     return ms_avg;
 }
 

@@ -1,0 +1,365 @@
+// Fused NOVA F(6,3) forward, block variant, for layers with few channels at
+// batch > 1: input transform, the 64 Winograd-domain MFMA products and the
+// output transform in one launch, with V in registers and M in LDS.
+//
+// The reference's fused kernel (/root/reference/csrc/nova_winograd_fused.hip:
+// 283-440) stages V for 16 tiles in LDS, multiplies with 16x16x16 MFMA and
+// keeps fp32 accumulators for 64 output channels; this kernel keeps that
+// output-stationary shape and re-plans the rest for gfx950 (160 KB LDS, one
+// workgroup of 8 waves per CU):
+//   * workgroup = 16 consecutive tiles of one image (row-major, so runs cross
+//     tile rows and no tile slot is wasted inside an image) x 64 output
+//     channels x all 64 positions; 8 waves (two per SIMD), wave w owns
+//     position row w (8 positions) and keeps its 128 fp32 accumulators in
+//     registers for the whole channel loop;
+//   * per 32-channel chunk the input rows that the run touches are staged in
+//     LDS as 16-byte-aligned row spans; every thread transforms one (channel,
+//     tile) patch (the full 8x8, 40 aligned LDS reads) and writes its 64
+//     positions into a V buffer laid out as v_mfma_f32_16x16x16_f16 B
+//     fragments (one conflict-free 8-byte read per lane and position);
+//   * each wave then multiplies its 8 positions: U fragments (A operands)
+//     straight from global/L2, two 16-channel k-steps per chunk;
+//   * after the channel loop, M (rounded to fp16, the reference's rounding
+//     point, nova_winograd_fused.hip:405) goes to LDS as [k][tile][position],
+//     and every thread runs the output transform for 2 (k, tile) pairs.
+// The transforms are the shared tile arithmetic (bit-identical to the
+// standalone kernels); products accumulate over 16-channel steps in order.
+#include <algorithm>
+
+#include "nova_internal.h"
+#include "nova_tables.h"
+#include "nova_tile_math.h"
+
+namespace nova {
+
+namespace {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef unsigned u2 __attribute__((ext_vector_type(2)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBT = 512;                            // threads per workgroup (8 waves)
+constexpr int kBCC = 32;                            // channels per chunk
+constexpr int kBMPitch = 72;                        // halves per (k, tile) row of M
+constexpr int kBLdsBytes = 160 * 1024;              // whole LDS: staging + V, later M
+constexpr int kBVBytes = 64 * kBCC * 16 * 2;        // 65536: V of one chunk
+constexpr int kBXBytes = kBLdsBytes - kBVBytes;     // 98304: staged input rows
+constexpr int kBOob = (int)0x80000000;
+
+struct BlockArgs {
+    const void* x_al;  // x rounded down to 16 bytes
+    const _Float16* U;  // fragment-ordered U
+    _Float16* y;
+    int x_bytes, xd, u_bytes, y_bytes;
+    int C, K, Cp, H, W, pad, nh, nw, Ho, Wo;
+    int P;        // tiles per image
+    int nruns;    // 16-tile runs per image
+    int n_kblk;   // 64-channel output blocks
+    int rp;       // bytes per staged row span
+    int cp;       // bytes per staged channel
+    int nj;       // 16-byte loads per row span
+    int chan2;    // (2*H*W) mod 16: span-alignment step per channel
+    int nkt, nks; // 16-row output tiles and 16-channel steps of the fragment-ordered U
+    int y_pairs;  // 1: store output pairs as 4-byte words (even Wo, 4-byte aligned y)
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+// V layout in LDS (halves): [position][k-step of 16 channels][channel group
+// of 4][tile][4 channels] -- the v_mfma_f32_16x16x16_f16 B fragment of lane l
+// (tile l % 16, channels 4*(l/16) .. +3) is one conflict-free 8-byte read.
+__device__ __forceinline__ int v_index(int pos, int c, int t) {
+    return (((pos * 2 + (c >> 4)) * 4 + ((c >> 2) & 3)) * 16 + t) * 4 + (c & 3);
+}
+
+// U fragments (A operands) of position row I at 16-channel step ks: 8
+// positions x 4 row tiles, read from the fragment-ordered copy of U (one
+// 512-byte contiguous fragment per wave load; zero padding built in). The
+// lane offset is the same for every fragment, the rest is a scalar offset.
+__device__ __forceinline__ void load_u(const BlockArgs& a, const __amdgpu_buffer_rsrc_t& urs,
+                                       int I, int kt0, int ks, int lane, h4 ua[8][4]) {
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int p = 8 * I + s;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            const int kt = kt0 + kb;
+            const int soff = kt < a.nkt ? ((p * a.nkt + kt) * a.nks + ks) * 512 : kBOob;
+            ua[s][kb] = __builtin_bit_cast(
+                h4, __builtin_amdgcn_raw_buffer_load_b64(urs, lane * 8, soff, 0));
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
+    __shared__ __align__(16) unsigned char lds[kBLdsBytes];
+    unsigned char* xs = lds;
+    _Float16* vs = reinterpret_cast<_Float16*>(lds + kBXBytes);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = position row
+
+    // ---- work item: (image b, 16-tile run, 64-channel output block) ----
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int kblk = L % a.n_kblk;
+    const int rest = L / a.n_kblk;
+    const int run = rest % a.nruns;
+    const int b = rest / a.nruns;
+    const int k0 = kblk * 64;
+    const int t0 = run * 16;
+    const int ntiles = min(16, a.P - t0);
+    const int th_first = t0 / a.nw;
+    const int nrows = (t0 + ntiles - 1) / a.nw - th_first + 1;
+    const int rows_st = 6 * nrows + 2;       // staged input rows
+    const int h_first = 6 * th_first - a.pad;
+    const int HW = a.H * a.W;
+    const __amdgpu_buffer_rsrc_t xrs = rsrc(a.x_al, a.x_bytes);
+    const __amdgpu_buffer_rsrc_t urs = rsrc(a.U, a.u_bytes);
+    const __amdgpu_buffer_rsrc_t yrs = rsrc(a.y, a.y_bytes);
+
+    // ---- transform role: channel ct = tid / 16 of the chunk, tile t ----
+    const int t = tid & 15;
+    const int ct = tid >> 4;
+    const bool tile_ok = t < ntiles;
+    const int tl = t0 + (tile_ok ? t : 0);
+    const int th = tl / a.nw, tw = tl - (tl / a.nw) * a.nw;
+    const int rb0 = 6 * (th - th_first) * a.rp + 12 * tw;
+    unsigned rr0 = 0, rmask = 0, cmask = 0;
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++) {
+        const int h = 6 * th - a.pad + ii;
+        rmask |= (tile_ok && h >= 0 && h < a.H) ? (1u << ii) : 0u;
+        rr0 |= (unsigned)((a.xd + 2 * (b * a.C * HW + h * a.W - a.pad)) & 15) << (4 * ii);
+        const int w = 6 * tw - a.pad + ii;
+        cmask |= (w >= 0 && w < a.W) ? (1u << ii) : 0u;
+    }
+
+    // ---- staging pieces: e = (channel c, staged row rs, 16-byte column j) ----
+    const int per_c = rows_st * a.nj;
+    const int total = kBCC * per_c;
+    const int e_c = tid / per_c;
+    const int e_rem = tid - e_c * per_c;
+    const int e_r = e_rem / a.nj;
+    const int e_j = e_rem - e_r * a.nj;
+    const int dc = kBT / per_c, drem = kBT - dc * per_c;
+    const int dr = drem / a.nj, dj = drem - dr * a.nj;
+
+    f4 acc[8][4];
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) acc[s][kb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int c0 = 0; c0 < a.Cp; c0 += kBCC) {
+        __syncthreads();  // the previous chunk is done with the staging area and V
+        // -- stage the chunk's input rows: four loads in flight per round --
+        {
+            int c = e_c, r = e_r, j = e_j;
+            for (int e = tid; e < total; e += 4 * kBT) {
+                u4 v[4];
+                int dst[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int h = h_first + r;
+                    const int cg = c0 + c;
+                    const bool ok = e + u * kBT < total && h >= 0 && h < a.H && cg < a.C;
+                    const int o = a.xd + 2 * ((b * a.C + cg) * HW + h * a.W - a.pad);
+                    v[u] = ok ? __builtin_amdgcn_raw_buffer_load_b128(xrs, (o & ~15) + 16 * j, 0, 0)
+                              : u4{0u, 0u, 0u, 0u};
+                    dst[u] = ok ? c * a.cp + r * a.rp + 16 * j : -1;
+                    j += dj;
+                    r += dr;
+                    c += dc;
+                    if (j >= a.nj) {
+                        j -= a.nj;
+                        r++;
+                    }
+                    if (r >= rows_st) {
+                        r -= rows_st;
+                        c++;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    if (dst[u] >= 0) *reinterpret_cast<u4*>(xs + dst[u]) = v[u];
+            }
+        }
+        __syncthreads();
+        // -- input transform of (channel c0 + ct, tile t) into V --
+        {
+            const int cg = c0 + ct;
+            const unsigned rm = cg < a.C ? rmask : 0u;
+            const unsigned char* cbase = xs + ct * a.cp + rb0;
+            unsigned d4[8][4];
+#pragma unroll
+            for (int ii = 0; ii < 8; ii++) {
+                const int rho = ((int)((rr0 >> (4 * ii)) & 15u) + cg * a.chan2) & 15;
+                const unsigned* src =
+                    reinterpret_cast<const unsigned*>(cbase + ii * a.rp + (rho & ~3));
+                unsigned w5[5];
+#pragma unroll
+                for (int q = 0; q < 5; q++) w5[q] = src[q];
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    d4[ii][q] = __builtin_amdgcn_alignbyte(w5[q + 1], w5[q], (unsigned)(rho & 3));
+            }
+            input_tile_rows(
+                [&](int ii, int j) {
+                    const unsigned pr = d4[ii][j >> 1];
+                    const unsigned short bits =
+                        (unsigned short)((j & 1) ? (pr >> 16) : (pr & 0xffffu));
+                    return ((rm >> ii) & (cmask >> j) & 1u)
+                               ? (float)__builtin_bit_cast(_Float16, bits)
+                               : 0.0f;
+                },
+                [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
+        }
+        __syncthreads();
+        // -- products: this wave's position row, two 16-channel k-steps --
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            h4 ua[8][4];
+            load_u(a, urs, wave, k0 / 16, (c0 >> 4) + ks, lane, ua);
+            h4 vf[8];
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                vf[s] = *reinterpret_cast<const h4*>(
+                    vs + ((((8 * wave + s) * 2 + ks) * 4 + (lane >> 4)) * 16 + (lane & 15)) * 4);
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+                    acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ua[s][kb], vf[s],
+                                                                       acc[s][kb], 0, 0, 0);
+        }
+    }
+    __syncthreads();  // staging area and V become M
+
+    // ---- M (fp16) to LDS: [kk][tile][position], one 16-byte write per
+    // (k, position row) of this lane ----
+    _Float16* ms = reinterpret_cast<_Float16*>(lds);
+    {
+        const int g = lane >> 4, tq = lane & 15;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = 16 * kb + 4 * g + i;
+                h8 v;
+#pragma unroll
+                for (int s = 0; s < 8; s++) v[s] = to_f16(acc[s][kb][i]);
+                *reinterpret_cast<h8*>(ms + (kk * 16 + tq) * kBMPitch + 8 * wave) = v;
+            }
+    }
+    __syncthreads();
+
+    // ---- output transform: (kk, tile) pairs, tile = tid % 16 ----
+    const bool pairs_w = a.y_pairs != 0;
+    for (int e = tid; e < 64 * 16; e += kBT) {
+        const int kk = e >> 4;
+        const int k = k0 + kk;
+        if (!tile_ok || k >= a.K) continue;
+        h8 mv[8];
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++)
+            mv[ii] = *reinterpret_cast<const h8*>(ms + (kk * 16 + t) * kBMPitch + 8 * ii);
+        float out[6][6];
+        output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
+        const int oh = th * 6, ow = tw * 6;
+        const int ybase = 2 * ((b * a.K + k) * a.Ho * a.Wo + ow);
+#pragma unroll
+        for (int r = 0; r < 6; r++) {
+            const int row = ybase + 2 * (oh + r) * a.Wo;
+            if (oh + r >= a.Ho) break;
+            if (pairs_w) {
+#pragma unroll
+                for (int s = 0; s < 6; s += 2) {
+                    if (ow + s < a.Wo) {
+                        const unsigned lo = __builtin_bit_cast(uint16_t, to_f16(out[r][s]));
+                        const unsigned hi = __builtin_bit_cast(uint16_t, to_f16(out[r][s + 1]));
+                        __builtin_amdgcn_raw_buffer_store_b32(lo | (hi << 16), yrs, row + 2 * s, 0,
+                                                              0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 6; s++)
+                    if (ow + s < a.Wo)
+                        __builtin_amdgcn_raw_buffer_store_b16(
+                            __builtin_bit_cast(uint16_t, to_f16(out[r][s])), yrs, row + 2 * s, 0, 0);
+            }
+        }
+    }
+}
+
+int round16i(int v) { return (v + 15) & ~15; }
+
+}  // namespace
+
+bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
+                      FusedBlockPlan* p) {
+    (void)Cp;
+    if (B < 1 || C < 1 || K < 1) return false;
+    const int P = nh * nw;
+    const int nruns = (P + 15) / 16;
+    int maxrows = 1;
+    for (int r = 0; r < nruns; r++) {
+        const int t0 = 16 * r, n = std::min(16, P - t0);
+        maxrows = std::max(maxrows, (t0 + n - 1) / nw - t0 / nw + 1);
+    }
+    const int rows_st = 6 * maxrows + 2;
+    const int rp = round16i(2 * (6 * nw + 2) + 18);
+    const int cp = rows_st * rp + 16;
+    if (kBCC * cp > kBXBytes) return false;
+    p->nruns = nruns;
+    p->n_kblk = (K + 63) / 64;
+    p->rp = rp;
+    p->cp = cp;
+    p->nj = rp / 16;
+    p->grid = (int64_t)B * nruns * p->n_kblk;
+    (void)H;
+    (void)W;
+    return p->grid < ((int64_t)1 << 31);
+}
+
+hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
+                              int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
+                              int Wo, const FusedBlockPlan& p, hipStream_t s) {
+    BlockArgs a;
+    const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
+    a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
+    a.xd = (int)(xp & 15);
+    a.x_bytes = (int)(2 * (int64_t)B * C * H * W + a.xd);
+    a.U = reinterpret_cast<const _Float16*>(U);
+    a.u_bytes = (int)(2 * u_frag_elems(K, Cp));
+    a.nkt = (K + 15) / 16;
+    a.nks = (Cp + 15) / 16;
+    a.y = reinterpret_cast<_Float16*>(y);
+    a.y_bytes = (int)(2 * (int64_t)B * K * Ho * Wo);
+    a.C = C;
+    a.K = K;
+    a.Cp = Cp;
+    a.H = H;
+    a.W = W;
+    a.pad = pad;
+    a.nh = nh;
+    a.nw = nw;
+    a.Ho = Ho;
+    a.Wo = Wo;
+    a.P = nh * nw;
+    a.nruns = p.nruns;
+    a.n_kblk = p.n_kblk;
+    a.rp = p.rp;
+    a.cp = p.cp;
+    a.nj = p.nj;
+    a.chan2 = (2 * H * W) & 15;
+    a.y_pairs = (Wo % 2 == 0 && (reinterpret_cast<uintptr_t>(y) & 3) == 0) ? 1 : 0;
+    fused_block_kernel<<<dim3((unsigned)p.grid), dim3(kBT), 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace nova

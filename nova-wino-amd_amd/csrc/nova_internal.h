@@ -33,6 +33,17 @@ hipError_t launch_filter_transform_ref(const float* w, uint16_t* U, int K, int C
 hipError_t launch_filter_transform_gemm(const float* w, uint16_t* U, int K, int C, int Cp,
                                         hipStream_t s);
 
+// Fragment-ordered copy of U for the fused kernels: for each position p, 16-row
+// output-channel tile kt and 16-channel step ks, the v_mfma_f32_16x16x16_f16 A
+// fragment as 64 lanes x 4 halves (lane = row + 16 * (channel % 16 / 4)), so a
+// wave reads one fragment as 512 contiguous bytes. Rows >= K and channels >= C
+// are zero. Uf[((p*nkt + kt)*nks + ks)*256 + lane*4 + e], nkt = ceil(K/16),
+// nks = ceil(Cp/16).
+inline int64_t u_frag_elems(int K, int Cp) {
+    return (int64_t)64 * ((K + 15) / 16) * ((Cp + 15) / 16) * 256;
+}
+hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStream_t s);
+
 // ---- input transform -----------------------------------------------------
 // V[p*pstride + bp*ldv + c], bp = (b*nh + th)*nw + tw, for th < nh, tw < nw.
 // Channels c in [C, ldv) are written as zero.
@@ -56,12 +67,34 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
 const char* wgemm_name(int K, int Cp, int BP);
 
 // ---- fused transform + GEMM + transform ------------------------------------
-// Returns false when the shape is outside the fused kernel's envelope.
-bool fused_supported(int K, int C);
+// Launch plan of the fused kernel for one shape: tile block (tbh x tbw tiles),
+// output-channel block (16*nm channels), staging geometry, grid and the
+// scratch it needs (M in fp16 and one uint32 counter per (tile block,
+// channel block), which must be zero before the first launch; every launch
+// leaves them zero).
+struct FusedPlan {
+    int tbh, tbw, nm, nbh, nbw, n_kb;
+    int rr, rp, cp, nj;
+    int64_t n_tb, grid, ms_bytes, cnt_count;
+};
+// False when the shape is outside the fused kernel's envelope.
+bool fused_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw, FusedPlan* p);
 bool fused_fits(int64_t x_elems, int64_t u_elems, int64_t y_elems);
-const char* fused_name(int K, int C, int64_t BP);
-hipError_t launch_fused(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
-                        int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
-                        int Wo, hipStream_t s);
+const char* fused_name(const FusedPlan& p);
+hipError_t launch_fused(const uint16_t* x, const uint16_t* U, uint16_t* y, uint16_t* Ms,
+                        unsigned* cnt, int B, int C, int K, int Cp, int H, int W, int pad,
+                        int nh, int nw, int Ho, int Wo, const FusedPlan& p, hipStream_t s);
+
+// Block variant (16-tile runs x 64 output channels x all positions per
+// workgroup, no scratch): layers with few channels at batch > 1.
+struct FusedBlockPlan {
+    int nruns, n_kblk, rp, cp, nj;
+    int64_t grid;
+};
+bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
+                      FusedBlockPlan* p);
+hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
+                              int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
+                              int Wo, const FusedBlockPlan& p, hipStream_t s);
 
 }  // namespace nova

@@ -97,6 +97,33 @@ __device__ __forceinline__ void input_tile_rows(Load ld, Store st) {
     }
 }
 
+// Row I of V = B^T d B for one patch (positions 8*I .. 8*I+7), with the same
+// per-element chains as input_tile_rows: t[j] over i ascending, then
+// v[I][s] over j ascending. Only the input rows i with B[i][I] != 0 are read.
+template <int I, typename Load>
+__device__ __forceinline__ void input_row(Load ld, float out[8]) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (kBh[i][I] != 0.0f) acc = __builtin_fmaf(kBh[i][I], ld(i, j), acc);
+        t[j] = acc;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (kBh[j][s] != 0.0f) acc = __builtin_fmaf(t[j], kBh[j][s], acc);
+        out[s] = acc;
+    }
+}
+
+// True when input row i enters row I of V (B[i][I] != 0).
+constexpr bool input_row_uses(int I, int i) { return kBh[i][I] != 0.0f; }
+
 // Output tile: ld(i, j) returns m[i][j] (position 8*i+j) as fp32.
 template <typename Load>
 __device__ __forceinline__ void output_tile(Load ld, float y[6][6]) {

@@ -80,6 +80,35 @@ hipError_t launch_filter_transform_gemm(const float* w, uint16_t* U, int K, int 
     return hipGetLastError();
 }
 
+// Reorder U[p][k][Cp] into MFMA A-fragment order (zero padded), one thread per
+// 4-channel lane slot.
+__global__ __launch_bounds__(256) void u_frag_kernel(const _Float16* __restrict__ U,
+                                                      _Float16* __restrict__ Uf, int K, int Cp,
+                                                      int nkt, int nks, int64_t nslots) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nslots) return;
+    const int lane = (int)(i & 63);
+    const int64_t frag = i >> 6;  // (p*nkt + kt)*nks + ks
+    const int ks = (int)(frag % nks);
+    const int kt = (int)((frag / nks) % nkt);
+    const int p = (int)(frag / ((int64_t)nks * nkt));
+    const int k = kt * 16 + (lane & 15);
+    const int c = ks * 16 + 4 * (lane >> 4);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 v = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+    if (k < K && c < Cp) v = *reinterpret_cast<const h4*>(U + ((int64_t)p * K + k) * Cp + c);
+    *reinterpret_cast<h4*>(Uf + i * 4) = v;
+}
+
+hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStream_t s) {
+    const int nkt = (K + 15) / 16, nks = (Cp + 15) / 16;
+    const int64_t nslots = (int64_t)64 * nkt * nks * 64;
+    u_frag_kernel<<<dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, s>>>(
+        reinterpret_cast<const _Float16*>(U), reinterpret_cast<_Float16*>(Uf), K, Cp, nkt, nks,
+        nslots);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Buffer-resource helpers. Every tensor is addressed through a raw buffer
 // resource: an offset at or past num_records reads 0 and drops stores, so
@@ -98,23 +127,33 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
 // ---------------------------------------------------------------------------
 // Input transform.
 // Workgroup = one tile row (th) x kInTW tiles along w x kInCB channels of one
-// image. Staging: each thread copies two full input rows (kInCols elements)
-// of the 8-row strip into LDS -- one vector offset per row, the column in the
-// load/store immediates; rows outside the image and channels past C read as
-// zeros through the buffer bounds. Compute: one (tile, channel) patch per
-// thread out of LDS (4-byte pair reads), 64 positions written with lanes over
-// consecutive channels (128 B per store instruction), position stride as a
-// scalar offset.
+// image (33 KB of LDS: four workgroups per CU). Staging: the strip's 8 input
+// rows of every channel are copied into LDS as whole 16-byte-aligned row spans
+// (kInNJ buffer loads per span; rows outside the image and channels past C are
+// stored as zeros). Compute: one (tile, channel) patch per thread, each row
+// read as five aligned dwords and shifted into place with v_alignbyte;
+// columns outside the image (zero padding, or neighbour-row bytes that the
+// aligned span picked up) are masked. The 64 positions are written with
+// lanes over consecutive channels (64 B runs per store instruction), the
+// position stride as a scalar offset.
 // ---------------------------------------------------------------------------
-constexpr int kInTW = 4;                   // tiles per workgroup along w
-constexpr int kInCB = 64;                  // channels per workgroup
-constexpr int kInCols = kInTW * 6 + 2;     // 26 input columns per strip
-constexpr int kInPlane = 8 * kInCols + 2;  // 210 halves per channel (odd dword stride)
+constexpr int kInTW = 8;                                   // tiles per workgroup along w
+constexpr int kInCB = 32;                                  // channels per workgroup
+constexpr int kInCols = kInTW * 6 + 2;                     // 50 input columns per strip
+constexpr int kInRP = ((2 * kInCols + 14 + 4) + 15) & ~15; // 128: bytes per staged row span
+                                                           // (50 columns, alignment slack,
+                                                           // one dword of read-ahead)
+constexpr int kInNJ = kInRP / 16;                          // 8 loads per span
+constexpr int kInCP = 8 * kInRP + 16;                      // 1040: channel pitch (16 x odd)
+constexpr int kInPieces = kInCB * 8 * kInNJ / 256;         // 8 loads per thread
+static_assert(kInCB * 8 * kInNJ % 256 == 0, "staging pieces must tile the workgroup");
+static_assert((kInCP / 16) % 2 == 1, "channel pitch must be an odd number of 16-byte units");
 
 __global__ __launch_bounds__(256) void input_transform_kernel(
-    const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
-    int nh, int nw, int ldv, int64_t pstride, int cblocks, int64_t x_bytes, int64_t v_bytes) {
-    __shared__ __align__(16) _Float16 sx[kInCB * kInPlane];
+    const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
+    int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int xd,
+    int64_t v_bytes) {
+    __shared__ __align__(16) unsigned char sx[kInCB * kInCP];
     // 1-D grid over (tile block, tile row, image x channel block), x fastest
     const int nwb = (nw + kInTW - 1) / kInTW;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -124,61 +163,80 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     const int b = bz / cblocks;
     const int c0 = (bz % cblocks) * kInCB;
     const int h0 = th * 6 - pad, w0 = tw0 * 6 - pad;
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, x_bytes);
+    const int HW = H * W;
+    // Byte offset (from x_al) of element (b, c0, h=0, w=w0). Spans start at
+    // the strip's first column even when it is left of the image (w0 < 0):
+    // offsets below 0 wrap past the buffer end and read zeros, and every
+    // compute read then lies at or after its span's start.
+    const int xbase = xd + 2 * ((b * C + c0) * HW + w0);
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x_al, x_bytes);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
 
-    // ---- staging: thread (row i, column col) copies its element for all 64
-    // channels. Lanes run along the row (two rows per wave: each load covers
-    // two 52-byte runs), the channel stride is a scalar offset, and row /
-    // column validity is folded into the vector offset (out of range -> 0). ----
+    // ---- staging: piece e = (channel c, row r, 16-byte column j16) ----
     {
-        const int i = threadIdx.x >> 5, col = threadIdx.x & 31;
-        if (col < kInCols) {
-            const int h = h0 + i, w = w0 + col;
-            const bool ok = h >= 0 && h < H && w >= 0 && w < W;
-            const int voff = ok ? 2 * (((b * C + c0) * H + h) * W + w) : kOob;
-            const int HW2 = 2 * H * W;
-            const int ncc = min(kInCB, C - c0);  // uniform
-            _Float16* sdst = sx + i * kInCols + col;
-            uint16_t v[kInCB];
-            if (ncc == kInCB) {  // full channel block: all 64 loads in flight at once
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        u4 val[kInPieces];
+        int lo[kInPieces];
 #pragma unroll
-                for (int u = 0; u < kInCB; u++)
-                    v[u] = __builtin_amdgcn_raw_buffer_load_b16(xrs, voff, u * HW2, 0);
-            } else {
-#pragma unroll
-                for (int u = 0; u < kInCB; u++)
-                    v[u] = u < ncc ? __builtin_amdgcn_raw_buffer_load_b16(xrs, voff, u * HW2, 0)
-                                   : (uint16_t)0;
-            }
-#pragma unroll
-            for (int u = 0; u < kInCB; u++) sdst[u * kInPlane] = __builtin_bit_cast(_Float16, v[u]);
+        for (int u = 0; u < kInPieces; u++) {
+            const int e = threadIdx.x + u * 256;
+            const int j16 = e % kInNJ;
+            const int rest = e / kInNJ;
+            const int r = rest % 8, c = rest / 8;
+            const int h = h0 + r;
+            const bool ok = h >= 0 && h < H && c0 + c < C;
+            const int o = xbase + 2 * (c * HW + h * W);
+            val[u] = ok ? __builtin_amdgcn_raw_buffer_load_b128(xrs, (o & ~15) + 16 * j16, 0, 0)
+                        : u4{0u, 0u, 0u, 0u};
+            lo[u] = c * kInCP + r * kInRP + 16 * j16;
         }
+#pragma unroll
+        for (int u = 0; u < kInPieces; u++) *reinterpret_cast<u4*>(sx + lo[u]) = val[u];
     }
     __syncthreads();
 
-    // ---- compute: (tile t, channel cc) per thread ----
-    const int cc = threadIdx.x & 63;
-    const int t = threadIdx.x >> 6;
+    // ---- compute: (tile t, channel cc) per thread; a wave covers 32
+    // channels of two adjacent tiles ----
+    const int cc = threadIdx.x & 31;
+    const int t = threadIdx.x >> 5;
     const int tw = tw0 + t;
     const int c = c0 + cc;
     const int bp = (b * nh + th) * nw + tw;
     const int voff = (tw < nw && c < ldv) ? 2 * (bp * ldv + c) : kOob;
-    const _Float16* sp = sx + cc * kInPlane + t * 6;
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    h2 d2[8][4];
+    unsigned cmask = 0;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int j = 0; j < 8; j++) {
+        const int w = w0 + 6 * t + j;
+        cmask |= (w >= 0 && w < W) ? (1u << j) : 0u;
+    }
+    // Row i of the patch: 8 halves at byte sb = rho + 12t of its span. Read
+    // the five aligned dwords from floor4(sb) and shift each output dword by
+    // (sb & 3) bytes (0 or 2) with v_alignbyte: aligned LDS reads only.
+    unsigned d4[8][4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
-            d2[i][jj] = *reinterpret_cast<const h2*>(sp + i * kInCols + 2 * jj);
-    input_tile_rows([&](int i, int j) { return (float)d2[i][j >> 1][j & 1]; },
-                    [&](int r, int s, float v) {
-                        const int p = r * 8 + s;
-                        __builtin_amdgcn_raw_buffer_store_b16(
-                            __builtin_bit_cast(uint16_t, to_f16(v)), vrs, voff,
-                            (int)(2 * p * pstride), 0);
-                    });
+    for (int i = 0; i < 8; i++) {
+        const int rho = (xbase + 2 * (cc * HW + (h0 + i) * W)) & 15;
+        const int sb = rho + 12 * t;
+        const unsigned* src = reinterpret_cast<const unsigned*>(sx + cc * kInCP + i * kInRP +
+                                                                (sb & ~3));
+        unsigned w5[5];
+#pragma unroll
+        for (int q = 0; q < 5; q++) w5[q] = src[q];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            d4[i][q] = __builtin_amdgcn_alignbyte(w5[q + 1], w5[q], (unsigned)(sb & 3));
+    }
+    input_tile_rows(
+        [&](int i, int j) {
+            const unsigned pair = d4[i][j >> 1];
+            const unsigned short bits = (unsigned short)((j & 1) ? (pair >> 16) : (pair & 0xffffu));
+            return ((cmask >> j) & 1u) ? (float)__builtin_bit_cast(_Float16, bits) : 0.0f;
+        },
+        [&](int r, int s, float v) {
+            const int p = r * 8 + s;
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, to_f16(v)), vrs,
+                                                  voff, (int)(2 * p * pstride), 0);
+        });
 }
 
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
@@ -187,9 +245,15 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     const int cblocks = (ldv + kInCB - 1) / kInCB;
     const int64_t nblocks = (int64_t)((nw + kInTW - 1) / kInTW) * nh * B * cblocks;
     if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
+    // x is addressed from the 16-byte boundary at or below it (same granule,
+    // so no byte outside x's pages is touched); offsets stay 32-bit.
+    const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
+    const int xd = (int)(xp & 15);
+    const int64_t x_bytes = 2 * (int64_t)B * C * H * W + xd;
+    if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     input_transform_kernel<<<dim3((unsigned)nblocks), dim3(256), 0, s>>>(
-        reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad, nh,
-        nw, ldv, pstride, cblocks, 2 * (int64_t)B * C * H * W, 2 * 64 * pstride);
+        reinterpret_cast<const void*>(xp - (uintptr_t)xd), reinterpret_cast<_Float16*>(V), C, H,
+        W, pad, nh, nw, ldv, pstride, cblocks, (int)x_bytes, xd, 2 * 64 * pstride);
     return hipGetLastError();
 }
 
@@ -197,17 +261,18 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
 // Output transform.
 // Workgroup = one tile row x kOutTW tiles x kOutKB output channels of one
 // image. Each thread reads the 64 positions of one (tile, k) (lanes over
-// consecutive k: coalesced; position stride as a scalar offset), computes the
-// 6x6 tile into LDS; the workgroup then writes whole output rows (one vector
-// offset per row, the column in the store immediate). Rows past Ho and
-// channels past K fall outside the buffer and are dropped; columns past Wo
-// are skipped with a workgroup-uniform bound.
+// consecutive k: coalesced; position stride as a scalar offset) and computes
+// its 6x6 tile into LDS; the workgroup then writes whole output row segments
+// of kVW halves per store (kVW = 4, 2 or 1, the widest the output row pitch
+// and base alignment allow). Blocks cut by the right edge of the image store
+// single halves. Rows past Ho and channels past K are skipped.
 // ---------------------------------------------------------------------------
 constexpr int kOutTW = 4;
 constexpr int kOutKB = 64;
 constexpr int kOutCols = kOutTW * 6;         // 24
-constexpr int kOutPlane = 6 * kOutCols + 2;  // 146 halves = 73 dwords (odd)
+constexpr int kOutPlane = 6 * kOutCols + 4;  // 148 halves: 8-byte aligned rows, 2-way writes
 
+template <int kVW>
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes) {
@@ -244,26 +309,54 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     }
     __syncthreads();
 
-    // ---- store: thread (row r, column col) writes its element for all 64
-    // channels: lanes run along the output row (two rows per wave), the
-    // channel stride is a scalar offset; rows past Ho / columns past the
-    // tile block or Wo fall outside and are dropped. ----
-    {
-        const int r = threadIdx.x >> 5, col = threadIdx.x & 31;
-        const int h = th * 6 + r, w = tw0 * 6 + col;
-        const int ncols = min(kOutCols, (nw - tw0) * 6);  // uniform
-        if (r < 6 && col < ncols) {
-            const bool ok = h < Ho && w < Wo;
-            const int yoff = ok ? 2 * (((b * K + k0) * Ho + h) * Wo + w) : kOob;
-            const int HoWo2 = 2 * Ho * Wo;
-            const int nkk = min(kOutKB, K - k0);  // uniform
-            const _Float16* ssrc = sy + r * kOutCols + col;
-#pragma unroll 16
-            for (int u = 0; u < kOutKB; u++) {
-                if (u < nkk)
-                    __builtin_amdgcn_raw_buffer_store_b16(
-                        __builtin_bit_cast(uint16_t, ssrc[u * kOutPlane]), yrs, yoff, u * HoWo2, 0);
+    // ---- store: e = (channel kk, row r, segment of kVW halves); a segment
+    // cut by the image's right edge is stored one half at a time ----
+    const int nkk = min(kOutKB, K - k0);            // uniform
+    const int ncols = min(kOutCols, Wo - tw0 * 6);  // uniform
+    const int h0 = th * 6;
+    const int nr = min(6, Ho - h0);                 // uniform
+    const int nseg = (ncols + kVW - 1) / kVW;       // uniform
+    const int per_k = nr * nseg;
+    const int total = nkk * per_k;
+    const int ybase = 2 * (((b * K + k0) * Ho + h0) * Wo + tw0 * 6);  // byte offset
+    // e advances by 256: decode once, then step (kk, r, sg) by carries
+    int e = threadIdx.x;
+    int kk = e / per_k;
+    int rem = e - kk * per_k;
+    int r = rem / nseg;
+    int sg = rem - r * nseg;
+    const int dk = 256 / per_k, drem = 256 - dk * per_k;
+    const int dr = drem / nseg, ds = drem - dr * nseg;
+    for (; e < total; e += 256) {
+        const _Float16* src = sy + kk * kOutPlane + r * kOutCols + sg * kVW;
+        const int off = ybase + 2 * ((kk * Ho + r) * Wo + sg * kVW);
+        if (sg * kVW + kVW <= ncols) {
+            if constexpr (kVW == 4) {
+                typedef unsigned u2 __attribute__((ext_vector_type(2)));
+                __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const u2*>(src), yrs, off,
+                                                      0, 0);
+            } else if constexpr (kVW == 2) {
+                __builtin_amdgcn_raw_buffer_store_b32(*reinterpret_cast<const unsigned*>(src),
+                                                      yrs, off, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_buffer_store_b16(*reinterpret_cast<const uint16_t*>(src),
+                                                      yrs, off, 0, 0);
             }
+        } else {
+            for (int q = 0; sg * kVW + q < ncols; q++)
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    *reinterpret_cast<const uint16_t*>(src + q), yrs, off + 2 * q, 0, 0);
+        }
+        sg += ds;
+        r += dr;
+        kk += dk;
+        if (sg >= nseg) {
+            sg -= nseg;
+            r++;
+        }
+        if (r >= nr) {
+            r -= nr;
+            kk++;
         }
     }
 }
@@ -274,9 +367,25 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
     const int kblocks = (K + kOutKB - 1) / kOutKB;
     const int64_t nblocks = (int64_t)((nw + kOutTW - 1) / kOutTW) * nh * B * kblocks;
     if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
-    output_transform_kernel<<<dim3((unsigned)nblocks), dim3(256), 0, s>>>(
-        reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
-        ldm, pstride, kblocks, 2 * 64 * pstride, 2 * (int64_t)B * K * Ho * Wo);
+    const int64_t y_bytes = 2 * (int64_t)B * K * Ho * Wo;
+    if (y_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
+    // widest row segment: every segment start must be aligned to its width
+    // (tw0*6 columns is a multiple of 24, so the row pitch decides)
+    const uintptr_t ya = reinterpret_cast<uintptr_t>(y);
+    const int vw = (Wo % 4 == 0 && ya % 8 == 0) ? 4 : (Wo % 2 == 0 && ya % 4 == 0) ? 2 : 1;
+    const dim3 grid((unsigned)nblocks), block(256);
+    const _Float16* Mh = reinterpret_cast<const _Float16*>(M);
+    _Float16* yh = reinterpret_cast<_Float16*>(y);
+    const int64_t m_bytes = 2 * 64 * pstride;
+    if (vw == 4)
+        output_transform_kernel<4><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+                                                          kblocks, m_bytes, y_bytes);
+    else if (vw == 2)
+        output_transform_kernel<2><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+                                                          kblocks, m_bytes, y_bytes);
+    else
+        output_transform_kernel<1><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+                                                          kblocks, m_bytes, y_bytes);
     return hipGetLastError();
 }
 

@@ -1,0 +1,132 @@
+"""Automatic path choice, full-size agreement between the pipelines, and HIP
+graph replay, through the C-ABI on the GPU.
+
+At BASELINE sizes the CPU oracle is too slow for every image, so the full
+B=32 layer is checked with size-independent properties: the automatically
+chosen path agrees with the three-pass pipeline (which is parity-tested
+against the oracle elsewhere) to within fp32 accumulation-order noise at the
+fp16 rounding of M, the first two images match the oracle itself, results
+are finite and bitwise repeatable, and graph replays reproduce the eager
+result exactly.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _lib():
+    from nova_winograd.ops import get_lib
+
+    return get_lib()
+
+
+def _check():
+    from nova_winograd.ops import check
+
+    check()
+
+
+def _kaiming(K, C):
+    g = torch.Generator().manual_seed(1)
+    w = torch.empty(K, C, 3, 3)
+    torch.nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu", generator=g)
+    return w
+
+
+def _forward(lib, path, x, w, pad):
+    B, C, H, W = x.shape
+    K = w.shape[0]
+    h = lib.nova_create()
+    try:
+        lib.nova_set_path(h, path)
+        lib.nova_set_weights(h, w.data_ptr(), K, C)
+        y = torch.empty(B, K, H + 2 * pad - 2, W + 2 * pad - 2, dtype=torch.float16, device=DEV)
+        lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, W, pad)
+        _check()
+        took = lib.nova_get_last_path(h)
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    return y, took
+
+
+# (B, C, K, H, expected automatic path)
+AUTO_CASES = [
+    (32, 64, 64, 56, 3),   # ResNet-50 conv2_x, B=32: fused tile-block kernel
+    (32, 128, 128, 28, 1),  # conv3_x: three-pass
+    (1, 64, 64, 56, 1),    # B=1: three-pass
+]
+
+
+@pytest.mark.parametrize("B,C,K,H,expect", AUTO_CASES)
+def test_auto_path_matches_three_pass(oracle, B, C, K, H, expect):
+    print(f"[dispatch] B={B} C={C} K={K} H={H}", flush=True)
+    lib = _lib()
+    torch.manual_seed(0)
+    x = torch.randn(B, C, H, H).half()
+    w = _kaiming(K, C)
+    xd, wd = x.to(DEV), w.to(DEV)
+    y_auto, took = _forward(lib, 0, xd, wd, 1)
+    assert took == expect
+    y_3p, took3 = _forward(lib, 1, xd, wd, 1)
+    assert took3 == 1
+    a = y_auto.float().cpu().numpy()
+    r = y_3p.float().cpu().numpy()
+    assert np.isfinite(a).all()
+    if expect == 1:
+        assert np.array_equal(y_auto.cpu().view(torch.int16).numpy(),
+                              y_3p.cpu().view(torch.int16).numpy())
+    else:
+        # same transforms, GEMM accumulated in 16- instead of 32-channel steps
+        rel = np.linalg.norm(a - r) / np.linalg.norm(r)
+        assert rel <= 2e-3, rel
+        assert np.abs(a - r).max() <= 0.1
+    # the first two images against the oracle
+    yo = oracle.conv2d(x[:2].numpy(), w.numpy(), 1)
+    assert oracle.rel_l2(a[:2].astype(np.float16), yo) <= 5e-3
+
+
+@pytest.mark.parametrize("path", [1, 3], ids=["3pass", "fused_block"])
+def test_graph_replay_matches_eager(path):
+    """A forward captured in a HIP graph replays to the eager result, with
+    eager work and synchronisation between replays."""
+    print(f"[graph] path={path}", flush=True)
+    lib = _lib()
+    B, C, K, H = 8, 64, 64, 56
+    torch.manual_seed(3)
+    x = torch.randn(B, C, H, H, device=DEV).half()
+    w = _kaiming(K, C).to(DEV)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_path(h, path)
+        lib.nova_set_weights(h, w.data_ptr(), K, C)
+        y_eager = torch.empty(B, K, H, H, dtype=torch.float16, device=DEV)
+        lib.nova_forward(h, x.data_ptr(), y_eager.data_ptr(), B, H, H, 1)
+        _check()
+        assert lib.nova_get_last_path(h) == path
+        torch.cuda.synchronize()
+        y = torch.empty_like(y_eager)
+        s = torch.cuda.Stream()
+        import ctypes
+
+        lib.nova_set_stream(h, ctypes.c_void_p(s.cuda_stream))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, H, 1)
+        _check()
+        for i in range(3):
+            y.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, y_eager), f"replay {i} differs"
+            # eager work between replays
+            z = torch.randn(1 << 20, device=DEV).sum()
+            torch.cuda.synchronize()
+            assert torch.isfinite(z)
+    finally:
+        lib.nova_destroy(h)
