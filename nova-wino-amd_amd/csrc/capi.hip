@@ -195,8 +195,7 @@ int64_t sub_batch(const Handle* Hd, const Shape& s) {
 
 bool fused_plan_for(const Handle* Hd, const Shape& s, FusedPlan* p) {
     const int64_t Bc = sub_batch(Hd, s);
-    if (s.pad > 16) return false;
-    if (!fused_fits(Bc * Hd->C * s.H * s.W, (int64_t)64 * Hd->K * Hd->Cp,
+    if (!fused_fits(Bc * Hd->C * s.H * s.W, u_frag_elems(Hd->K, Hd->Cp),
                     Bc * Hd->K * s.Ho * s.Wo))
         return false;
     return fused_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.nh, s.nw, p);
@@ -351,7 +350,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
         } else if (path == 2) {
             const hipStream_t st = Hd->stream;
-            const uint16_t* U = Hd->U;
+            const uint16_t* U = Hd->Uf;
             const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
             FusedPlan fp;
             if (!fused_plan((int)s.B, C, K, Cp, s.H, s.W, s.nh, s.nw, &fp)) {

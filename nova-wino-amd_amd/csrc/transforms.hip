@@ -126,42 +126,50 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
 
 // ---------------------------------------------------------------------------
 // Input transform.
-// Workgroup = one tile row (th) x kInTW tiles along w x kInCB channels of one
-// image (33 KB of LDS: four workgroups per CU). Staging: the strip's 8 input
+// Workgroup (256 threads) = one tile row (th) x TW tiles along w x 256/TW
+// channels of one image; TW (2, 4 or 8) is picked per layer so that padded
+// tile and channel slots waste the least work. Staging: the strip's 8 input
 // rows of every channel are copied into LDS as whole 16-byte-aligned row spans
-// (kInNJ buffer loads per span; rows outside the image and channels past C are
-// stored as zeros). Compute: one (tile, channel) patch per thread, each row
-// read as five aligned dwords and shifted into place with v_alignbyte;
+// (one buffer load per 16 bytes; rows outside the image and channels past C
+// are stored as zeros). Compute: one (tile, channel) patch per thread, each
+// row read as five aligned dwords and shifted into place with v_alignbyte;
 // columns outside the image (zero padding, or neighbour-row bytes that the
-// aligned span picked up) are masked. The 64 positions are written with
-// lanes over consecutive channels (64 B runs per store instruction), the
-// position stride as a scalar offset.
+// aligned span picked up) are masked. The 64 positions are written with lanes
+// over consecutive channels, the position stride as a scalar offset.
 // ---------------------------------------------------------------------------
-constexpr int kInTW = 8;                                   // tiles per workgroup along w
-constexpr int kInCB = 32;                                  // channels per workgroup
-constexpr int kInCols = kInTW * 6 + 2;                     // 50 input columns per strip
-constexpr int kInRP = ((2 * kInCols + 14 + 4) + 15) & ~15; // 128: bytes per staged row span
-                                                           // (50 columns, alignment slack,
-                                                           // one dword of read-ahead)
-constexpr int kInNJ = kInRP / 16;                          // 8 loads per span
-constexpr int kInCP = 8 * kInRP + 16;                      // 1040: channel pitch (16 x odd)
-constexpr int kInPieces = kInCB * 8 * kInNJ / 256;         // 8 loads per thread
-static_assert(kInCB * 8 * kInNJ % 256 == 0, "staging pieces must tile the workgroup");
-static_assert((kInCP / 16) % 2 == 1, "channel pitch must be an odd number of 16-byte units");
+template <int TW>
+struct InGeom {
+    static constexpr int kCB = 256 / TW;                           // channels per workgroup
+    static constexpr int kCols = TW * 6 + 2;                       // input columns per strip
+    static constexpr int kRP = ((2 * kCols + 14 + 4) + 15) & ~15;  // bytes per row span (columns,
+                                                                   // alignment slack, one dword
+                                                                   // of read-ahead)
+    static constexpr int kNJ = kRP / 16;                           // loads per span
+    // Channel pitch 8 x odd: lanes over consecutive channels then hit at most
+    // two channels per LDS bank (staging writes are 8-byte halves).
+    static constexpr int kCP = 8 * kRP + 8;
+    static constexpr int kPieces = kCB * 8 * kNJ / 256;            // loads per thread
+    static constexpr int kBytes = kCB * kCP;
+    static_assert(kCB * 8 * kNJ % 256 == 0, "staging pieces must tile the workgroup");
+    static_assert((kCP / 8) % 2 == 1, "channel pitch must be an odd number of 8-byte units");
+    __device__ static int base(int c) { return c * kCP; }
+};
 
+template <int TW>
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int xd,
     int64_t v_bytes) {
-    __shared__ __align__(16) unsigned char sx[kInCB * kInCP];
+    using G = InGeom<TW>;
+    __shared__ __align__(16) unsigned char sx[G::kBytes];
     // 1-D grid over (tile block, tile row, image x channel block), x fastest
-    const int nwb = (nw + kInTW - 1) / kInTW;
+    const int nwb = (nw + TW - 1) / TW;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int tw0 = (L % nwb) * kInTW;
+    const int tw0 = (L % nwb) * TW;
     const int th = (L / nwb) % nh;
     const int bz = L / (nwb * nh);
     const int b = bz / cblocks;
-    const int c0 = (bz % cblocks) * kInCB;
+    const int c0 = (bz % cblocks) * G::kCB;
     const int h0 = th * 6 - pad, w0 = tw0 * 6 - pad;
     const int HW = H * W;
     // Byte offset (from x_al) of element (b, c0, h=0, w=w0). Spans start at
@@ -175,30 +183,33 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     // ---- staging: piece e = (channel c, row r, 16-byte column j16) ----
     {
         typedef unsigned u4 __attribute__((ext_vector_type(4)));
-        u4 val[kInPieces];
-        int lo[kInPieces];
+        u4 val[G::kPieces];
+        int lo[G::kPieces];
 #pragma unroll
-        for (int u = 0; u < kInPieces; u++) {
+        for (int u = 0; u < G::kPieces; u++) {
             const int e = threadIdx.x + u * 256;
-            const int j16 = e % kInNJ;
-            const int rest = e / kInNJ;
+            const int j16 = e % G::kNJ;
+            const int rest = e / G::kNJ;
             const int r = rest % 8, c = rest / 8;
             const int h = h0 + r;
             const bool ok = h >= 0 && h < H && c0 + c < C;
             const int o = xbase + 2 * (c * HW + h * W);
             val[u] = ok ? __builtin_amdgcn_raw_buffer_load_b128(xrs, (o & ~15) + 16 * j16, 0, 0)
                         : u4{0u, 0u, 0u, 0u};
-            lo[u] = c * kInCP + r * kInRP + 16 * j16;
+            lo[u] = G::base(c) + r * G::kRP + 16 * j16;
         }
+        typedef unsigned u2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int u = 0; u < kInPieces; u++) *reinterpret_cast<u4*>(sx + lo[u]) = val[u];
+        for (int u = 0; u < G::kPieces; u++) {
+            *reinterpret_cast<u2*>(sx + lo[u]) = u2{val[u][0], val[u][1]};
+            *reinterpret_cast<u2*>(sx + lo[u] + 8) = u2{val[u][2], val[u][3]};
+        }
     }
     __syncthreads();
 
-    // ---- compute: (tile t, channel cc) per thread; a wave covers 32
-    // channels of two adjacent tiles ----
-    const int cc = threadIdx.x & 31;
-    const int t = threadIdx.x >> 5;
+    // ---- compute: (tile t, channel cc) per thread, lanes over channels ----
+    const int cc = threadIdx.x % G::kCB;
+    const int t = threadIdx.x / G::kCB;
     const int tw = tw0 + t;
     const int c = c0 + cc;
     const int bp = (b * nh + th) * nw + tw;
@@ -217,7 +228,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     for (int i = 0; i < 8; i++) {
         const int rho = (xbase + 2 * (cc * HW + (h0 + i) * W)) & 15;
         const int sb = rho + 12 * t;
-        const unsigned* src = reinterpret_cast<const unsigned*>(sx + cc * kInCP + i * kInRP +
+        const unsigned* src = reinterpret_cast<const unsigned*>(sx + G::base(cc) + i * G::kRP +
                                                                 (sb & ~3));
         unsigned w5[5];
 #pragma unroll
@@ -239,11 +250,37 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
         });
 }
 
+// Tile-block width for a transform over rows x n tile columns and ch
+// channels with 256/TW channels per workgroup. Small problems (the widest
+// grid still under 256 workgroups, e.g. batch 1) take the widest grid, since
+// their time is one workgroup's latency; otherwise the least padded work,
+// ties to the wider block.
+static int pick_tw(int64_t rows, int n, int ch) {
+    int best = 8, widest = 8;
+    int64_t best_w = -1, widest_g = -1;
+    for (int tw = 8; tw >= 2; tw /= 2) {
+        const int cb = 256 / tw;
+        const int64_t nb = (int64_t)((n + tw - 1) / tw) * ((ch + cb - 1) / cb);
+        const int64_t w = nb * tw * cb;
+        if (best_w < 0 || w < best_w) {
+            best_w = w;
+            best = tw;
+        }
+        if (nb * rows > widest_g) {
+            widest_g = nb * rows;
+            widest = tw;
+        }
+    }
+    return widest_g < 256 ? widest : best;
+}
+
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
                                   hipStream_t s) {
-    const int cblocks = (ldv + kInCB - 1) / kInCB;
-    const int64_t nblocks = (int64_t)((nw + kInTW - 1) / kInTW) * nh * B * cblocks;
+    const int tw = pick_tw((int64_t)B * nh, nw, ldv);
+    const int cb = 256 / tw;
+    const int cblocks = (ldv + cb - 1) / cb;
+    const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * cblocks;
     if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
     // x is addressed from the 16-byte boundary at or below it (same granule,
     // so no byte outside x's pages is touched); offsets stay 32-bit.
@@ -251,45 +288,67 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     const int xd = (int)(xp & 15);
     const int64_t x_bytes = 2 * (int64_t)B * C * H * W + xd;
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
-    input_transform_kernel<<<dim3((unsigned)nblocks), dim3(256), 0, s>>>(
-        reinterpret_cast<const void*>(xp - (uintptr_t)xd), reinterpret_cast<_Float16*>(V), C, H,
-        W, pad, nh, nw, ldv, pstride, cblocks, (int)x_bytes, xd, 2 * 64 * pstride);
+    const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
+    _Float16* Vh = reinterpret_cast<_Float16*>(V);
+    const dim3 grid((unsigned)nblocks), block(256);
+    switch (tw) {
+        case 2:
+            input_transform_kernel<2><<<grid, block, 0, s>>>(xa, Vh, C, H, W, pad, nh, nw, ldv,
+                                                             pstride, cblocks, (int)x_bytes, xd,
+                                                             2 * 64 * pstride);
+            break;
+        case 4:
+            input_transform_kernel<4><<<grid, block, 0, s>>>(xa, Vh, C, H, W, pad, nh, nw, ldv,
+                                                             pstride, cblocks, (int)x_bytes, xd,
+                                                             2 * 64 * pstride);
+            break;
+        default:
+            input_transform_kernel<8><<<grid, block, 0, s>>>(xa, Vh, C, H, W, pad, nh, nw, ldv,
+                                                             pstride, cblocks, (int)x_bytes, xd,
+                                                             2 * 64 * pstride);
+            break;
+    }
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // Output transform.
-// Workgroup = one tile row x kOutTW tiles x kOutKB output channels of one
-// image. Each thread reads the 64 positions of one (tile, k) (lanes over
-// consecutive k: coalesced; position stride as a scalar offset) and computes
-// its 6x6 tile into LDS; the workgroup then writes whole output row segments
-// of kVW halves per store (kVW = 4, 2 or 1, the widest the output row pitch
-// and base alignment allow). Blocks cut by the right edge of the image store
-// single halves. Rows past Ho and channels past K are skipped.
+// Workgroup (256 threads) = one tile row x TW tiles x 256/TW output channels of
+// one image (TW picked per layer like the input transform). Each thread reads
+// the 64 positions of one (tile, k) (lanes over consecutive k: coalesced;
+// position stride as a scalar offset) and computes its 6x6 tile into LDS; the
+// workgroup then writes whole output row segments of kVW halves per store
+// (kVW = 4, 2 or 1, the widest the output row pitch and base alignment allow).
+// A segment cut by the right edge of the image is stored one half at a time;
+// rows past Ho and channels past K are skipped.
 // ---------------------------------------------------------------------------
-constexpr int kOutTW = 4;
-constexpr int kOutKB = 64;
-constexpr int kOutCols = kOutTW * 6;         // 24
-constexpr int kOutPlane = 6 * kOutCols + 4;  // 148 halves: 8-byte aligned rows, 2-way writes
+template <int TW>
+struct OutGeom {
+    static constexpr int kKB = 256 / TW;          // output channels per workgroup
+    static constexpr int kCols = TW * 6;          // output columns per block
+    static constexpr int kPlane = 6 * kCols + 4;  // halves per channel: 8-byte rows,
+                                                  // at most 2-way write conflicts
+};
 
-template <int kVW>
+template <int TW, int kVW>
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes) {
-    __shared__ __align__(16) _Float16 sy[kOutKB * kOutPlane];
-    const int nwb = (nw + kOutTW - 1) / kOutTW;
+    using G = OutGeom<TW>;
+    __shared__ __align__(16) _Float16 sy[G::kKB * G::kPlane];
+    const int nwb = (nw + TW - 1) / TW;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int tw0 = (L % nwb) * kOutTW;
+    const int tw0 = (L % nwb) * TW;
     const int th = (L / nwb) % nh;
     const int bz = L / (nwb * nh);
     const int b = bz / kblocks;
-    const int k0 = (bz % kblocks) * kOutKB;
+    const int k0 = (bz % kblocks) * G::kKB;
     const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, m_bytes);
     const __amdgpu_buffer_rsrc_t yrs = make_rsrc(y, y_bytes);
 
     {
-        const int kk = threadIdx.x & 63;
-        const int t = threadIdx.x >> 6;
+        const int kk = threadIdx.x % G::kKB;
+        const int t = threadIdx.x / G::kKB;
         const int tw = tw0 + t;
         const int k = k0 + kk;
         const int bp = (b * nh + th) * nw + tw;
@@ -301,21 +360,20 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
         float out[6][6];
         output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
                     out);
-        _Float16* sp = sy + kk * kOutPlane + t * 6;
+        _Float16* sp = sy + kk * G::kPlane + t * 6;
 #pragma unroll
         for (int r = 0; r < 6; r++)
 #pragma unroll
-            for (int s = 0; s < 6; s++) sp[r * kOutCols + s] = to_f16(out[r][s]);
+            for (int s = 0; s < 6; s++) sp[r * G::kCols + s] = to_f16(out[r][s]);
     }
     __syncthreads();
 
-    // ---- store: e = (channel kk, row r, segment of kVW halves); a segment
-    // cut by the image's right edge is stored one half at a time ----
-    const int nkk = min(kOutKB, K - k0);            // uniform
-    const int ncols = min(kOutCols, Wo - tw0 * 6);  // uniform
+    // ---- store: e = (channel kk, row r, segment of kVW halves) ----
+    const int nkk = min(G::kKB, K - k0);              // uniform
+    const int ncols = min(G::kCols, Wo - tw0 * 6);    // uniform
     const int h0 = th * 6;
-    const int nr = min(6, Ho - h0);                 // uniform
-    const int nseg = (ncols + kVW - 1) / kVW;       // uniform
+    const int nr = min(6, Ho - h0);                   // uniform
+    const int nseg = (ncols + kVW - 1) / kVW;         // uniform
     const int per_k = nr * nseg;
     const int total = nkk * per_k;
     const int ybase = 2 * (((b * K + k0) * Ho + h0) * Wo + tw0 * 6);  // byte offset
@@ -328,7 +386,7 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     const int dk = 256 / per_k, drem = 256 - dk * per_k;
     const int dr = drem / nseg, ds = drem - dr * nseg;
     for (; e < total; e += 256) {
-        const _Float16* src = sy + kk * kOutPlane + r * kOutCols + sg * kVW;
+        const _Float16* src = sy + kk * G::kPlane + r * G::kCols + sg * kVW;
         const int off = ybase + 2 * ((kk * Ho + r) * Wo + sg * kVW);
         if (sg * kVW + kVW <= ncols) {
             if constexpr (kVW == 4) {
@@ -361,31 +419,54 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     }
 }
 
+template <int TW>
+static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, _Float16* yh,
+                          int K, int Ho, int Wo, int nh, int nw, int ldm, int64_t pstride,
+                          int kblocks, int64_t m_bytes, int64_t y_bytes) {
+    const dim3 block(256);
+    if (vw == 4)
+        output_transform_kernel<TW, 4><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm,
+                                                              pstride, kblocks, m_bytes, y_bytes);
+    else if (vw == 2)
+        output_transform_kernel<TW, 2><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm,
+                                                              pstride, kblocks, m_bytes, y_bytes);
+    else
+        output_transform_kernel<TW, 1><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm,
+                                                              pstride, kblocks, m_bytes, y_bytes);
+}
+
 hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K, int Ho,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
                                    hipStream_t s) {
-    const int kblocks = (K + kOutKB - 1) / kOutKB;
-    const int64_t nblocks = (int64_t)((nw + kOutTW - 1) / kOutTW) * nh * B * kblocks;
+    const int tw = pick_tw((int64_t)B * nh, nw, K);
+    const int kb = 256 / tw;
+    const int kblocks = (K + kb - 1) / kb;
+    const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * kblocks;
     if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
     const int64_t y_bytes = 2 * (int64_t)B * K * Ho * Wo;
     if (y_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     // widest row segment: every segment start must be aligned to its width
-    // (tw0*6 columns is a multiple of 24, so the row pitch decides)
+    // (tw0*6 columns is a multiple of 12, so the row pitch decides)
     const uintptr_t ya = reinterpret_cast<uintptr_t>(y);
     const int vw = (Wo % 4 == 0 && ya % 8 == 0) ? 4 : (Wo % 2 == 0 && ya % 4 == 0) ? 2 : 1;
-    const dim3 grid((unsigned)nblocks), block(256);
+    const dim3 grid((unsigned)nblocks);
     const _Float16* Mh = reinterpret_cast<const _Float16*>(M);
     _Float16* yh = reinterpret_cast<_Float16*>(y);
     const int64_t m_bytes = 2 * 64 * pstride;
-    if (vw == 4)
-        output_transform_kernel<4><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                                                          kblocks, m_bytes, y_bytes);
-    else if (vw == 2)
-        output_transform_kernel<2><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                                                          kblocks, m_bytes, y_bytes);
-    else
-        output_transform_kernel<1><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                                                          kblocks, m_bytes, y_bytes);
+    switch (tw) {
+        case 2:
+            launch_out_tw<2>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+                             m_bytes, y_bytes);
+            break;
+        case 4:
+            launch_out_tw<4>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+                             m_bytes, y_bytes);
+            break;
+        default:
+            launch_out_tw<8>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+                             m_bytes, y_bytes);
+            break;
+    }
     return hipGetLastError();
 }
 
