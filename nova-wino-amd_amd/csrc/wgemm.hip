@@ -151,7 +151,7 @@ static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 constexpr int kStageC = 64;
 constexpr int kPitch = 72;
 
-template <int TK, int TB, int WK, int WB>
+template <int TK, int TB, int WK, int WB, int PF>
 __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restrict__ U,
                                                         const _Float16* __restrict__ V,
                                                         _Float16* __restrict__ M, int K, int Cp,
@@ -200,31 +200,33 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         vlds[j] = ch < kChunksV ? row * kPitch + cg * 8 : -1;
     }
     const int nstages = (Cp + kStageC - 1) / kStageC;
-    h8 ru[kPerThreadU], rv[kPerThreadV];
-    auto gload = [&](int st) {
+    // PF stages in flight in registers: slot st % PF holds stage st from its
+    // load until its copy into LDS
+    h8 ru[PF][kPerThreadU], rv[PF][kPerThreadV];
+    auto gload = [&](int st, h8 (&u)[kPerThreadU], h8 (&v)[kPerThreadV]) {
         const int c = st * kStageC;
 #pragma unroll
         for (int j = 0; j < kPerThreadU; j++) {
             const int cg = (tid + j * 256) & 7;
             const bool cok = c + cg * 8 < Cp;
-            ru[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
-                                               urs, cok ? uoff[j] : kOob, au + 2 * c, 0));
+            u[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              urs, cok ? uoff[j] : kOob, au + 2 * c, 0));
         }
 #pragma unroll
         for (int j = 0; j < kPerThreadV; j++) {
             const int cg = (tid + j * 256) & 7;
             const bool cok = c + cg * 8 < Cp;
-            rv[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
-                                               vrs, cok ? voff[j] : kOob, bu + 2 * c, 0));
+            v[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                              vrs, cok ? voff[j] : kOob, bu + 2 * c, 0));
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, const h8 (&u)[kPerThreadU], const h8 (&v)[kPerThreadV]) {
 #pragma unroll
         for (int j = 0; j < kPerThreadU; j++)
-            if (ulds[j] >= 0) *reinterpret_cast<h8*>(&sU[buf][ulds[j]]) = ru[j];
+            if (ulds[j] >= 0) *reinterpret_cast<h8*>(&sU[buf][ulds[j]]) = u[j];
 #pragma unroll
         for (int j = 0; j < kPerThreadV; j++)
-            if (vlds[j] >= 0) *reinterpret_cast<h8*>(&sV[buf][vlds[j]]) = rv[j];
+            if (vlds[j] >= 0) *reinterpret_cast<h8*>(&sV[buf][vlds[j]]) = v[j];
     };
 
     f4 acc[MT][NT];
@@ -233,32 +235,39 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
 #pragma unroll
         for (int ni = 0; ni < NT; ni++) acc[mi][ni] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    gload(0);
-    lstore(0);
+#pragma unroll
+    for (int j = 0; j < PF; j++)
+        if (j < nstages) gload(j, ru[j], rv[j]);
+    lstore(0, ru[0], rv[0]);
     __syncthreads();
-    for (int st = 0; st < nstages; st++) {
-        const int buf = st & 1;
-        if (st + 1 < nstages) gload(st + 1);
-        const _Float16* su = sU[buf] + (wk * MT * 16 + r16) * kPitch + 8 * g;
-        const _Float16* sv = sV[buf] + (wb * NT * 16 + r16) * kPitch + 8 * g;
+    for (int st0 = 0; st0 < nstages; st0 += PF) {
 #pragma unroll
-        for (int kk = 0; kk < kStageC / 32; kk++) {
-            h8 a[MT], b[NT];
+        for (int j = 0; j < PF; j++) {
+            const int st = st0 + j;
+            if (st >= nstages) break;
+            const int buf = st & 1;
+            if (st + PF < nstages) gload(st + PF, ru[j], rv[j]);
+            const _Float16* su = sU[buf] + (wk * MT * 16 + r16) * kPitch + 8 * g;
+            const _Float16* sv = sV[buf] + (wb * NT * 16 + r16) * kPitch + 8 * g;
 #pragma unroll
-            for (int mi = 0; mi < MT; mi++)
-                a[mi] = *reinterpret_cast<const h8*>(su + mi * 16 * kPitch + kk * 32);
+            for (int kk = 0; kk < kStageC / 32; kk++) {
+                h8 a[MT], b[NT];
 #pragma unroll
-            for (int ni = 0; ni < NT; ni++)
-                b[ni] = *reinterpret_cast<const h8*>(sv + ni * 16 * kPitch + kk * 32);
-#pragma unroll
-            for (int mi = 0; mi < MT; mi++)
+                for (int mi = 0; mi < MT; mi++)
+                    a[mi] = *reinterpret_cast<const h8*>(su + mi * 16 * kPitch + kk * 32);
 #pragma unroll
                 for (int ni = 0; ni < NT; ni++)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mi], b[ni],
-                                                                         acc[mi][ni], 0, 0, 0);
+                    b[ni] = *reinterpret_cast<const h8*>(sv + ni * 16 * kPitch + kk * 32);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+                    for (int ni = 0; ni < NT; ni++)
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mi], b[ni],
+                                                                             acc[mi][ni], 0, 0, 0);
+            }
+            if (st + 1 < nstages) lstore(buf ^ 1, ru[(j + 1) % PF], rv[(j + 1) % PF]);
+            __syncthreads();
         }
-        if (st + 1 < nstages) lstore(buf ^ 1);
-        __syncthreads();
     }
 
     const int mu = 2 * p * BP * K;
@@ -285,11 +294,11 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         }
 }
 
-template <int TK, int TB, int WK, int WB>
+template <int TK, int TB, int WK, int WB, int PF>
 static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                              int BP, hipStream_t s) {
     dim3 grid((unsigned)((BP + TB - 1) / TB), (unsigned)((K + TK - 1) / TK), 64);
-    wgemm_lds_kernel<TK, TB, WK, WB><<<grid, dim3(256), 0, s>>>(
+    wgemm_lds_kernel<TK, TB, WK, WB, PF><<<grid, dim3(256), 0, s>>>(
         reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
         reinterpret_cast<_Float16*>(M), K, Cp, BP);
     return hipGetLastError();
@@ -316,8 +325,8 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
                         int BP, hipStream_t s) {
     switch (wgemm_cfg(K, BP)) {
         case 0: return launch_cfg<1, 1, 4, 1, 4>(U, V, M, K, Cp, BP, s);
-        case 1: return launch_lds<64, 64, 2, 2>(U, V, M, K, Cp, BP, s);
-        default: return launch_lds<128, 128, 2, 2>(U, V, M, K, Cp, BP, s);
+        case 1: return launch_lds<64, 64, 2, 2, 1>(U, V, M, K, Cp, BP, s);
+        default: return launch_lds<128, 128, 2, 2, 1>(U, V, M, K, Cp, BP, s);
     }
 }
 
