@@ -116,6 +116,13 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
  * tile-block kernel (few channels, batch > 1). A forced fused path outside its
  * envelope runs 3-pass and reports an error. */
 NOVA_API void nova_set_path(nova_handle_t h, int path);
+/* Output epilogue of every subsequent forward on the handle: d_bias_f16 is a
+ * device array of K fp16 values added per output channel (NULL: none), with
+ * the rounding of the reference's separate `y + bias.half()`; relu = 1 clamps
+ * negative outputs to zero. No counterpart in the reference, whose bias is a
+ * separate elementwise op after the convolution
+ * (/root/reference/nova_winograd/conv2d.py:240-241). */
+NOVA_API void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu);
 /* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused
  * (position rows), 3 = fused (tile blocks). */
 NOVA_API int nova_get_last_path(nova_handle_t h);

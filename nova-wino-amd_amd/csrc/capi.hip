@@ -78,6 +78,7 @@ struct Handle {
     size_t cnt_cap = 0;       // counters
     hipStream_t stream = nullptr;
     int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block
+    Epilogue ep;        // bias / ReLU applied by every forward
     int last_path = 0;
     bool ready = false;
     Profiler prof;
@@ -244,9 +245,10 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
                                       (int64_t)Cp * s.BP, st);
     };
     auto gm = [=]() { return launch_wgemm(U, V, M, K, Cp, (int)s.BP, st); };
+    const Epilogue ep = Hd->ep;
     auto out = [=]() {
         return launch_output_transform(M, y, s.B, K, s.Ho, s.Wo, s.nh, s.nw, K,
-                                       (int64_t)K * s.BP, st);
+                                       (int64_t)K * s.BP, st, ep);
     };
     if (remember) {
         pf.last[kKindInput] = in;
@@ -336,9 +338,10 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
                 return;
             }
+            const Epilogue ep = Hd->ep;
             auto fz = [=]() {
                 return launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
-                                          s.Ho, s.Wo, bp, st);
+                                          s.Ho, s.Wo, bp, st, ep);
             };
             if (b0 == 0) {
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
@@ -361,9 +364,10 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 return;
             uint16_t* Ms = static_cast<uint16_t*>(Hd->ws);
             unsigned* cnt = Hd->cnt;
+            const Epilogue ep = Hd->ep;
             auto fz = [=]() {
                 return launch_fused(xx, U, yy, Ms, cnt, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh,
-                                    s.nw, s.Ho, s.Wo, fp, st);
+                                    s.nw, s.Ho, s.Wo, fp, st, ep);
             };
             if (b0 == 0) {
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
@@ -585,6 +589,17 @@ void nova_set_path(nova_handle_t h, int path) {
         return;
     }
     H->path_pref = path;
+}
+
+void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu) {
+    Handle* H = as_handle(h, "nova_set_epilogue");
+    if (!H) return;
+    if (relu != 0 && relu != 1) {
+        set_error(kErrInvalidArgument, "nova_set_epilogue: relu must be 0 or 1");
+        return;
+    }
+    H->ep.bias = static_cast<const uint16_t*>(d_bias_f16);
+    H->ep.relu = relu;
 }
 
 int nova_get_last_path(nova_handle_t h) {

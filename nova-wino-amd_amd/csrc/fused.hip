@@ -63,6 +63,8 @@ struct FusedArgs {
     int tbh, tbw, nbh, nbw, n_kb;
     int rr, rp, cp, nj;  // staging geometry: rows, row pitch, channel pitch (bytes), loads/row
     int nkt, nks;        // 16-row tiles / 16-channel steps of the fragment-ordered U
+    const _Float16* bias;  // output epilogue (null: none)
+    int relu;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -358,8 +360,8 @@ __global__ __launch_bounds__(kFThreads, 1) void fused_kernel(FusedArgs a) {
             for (int ss = 0; ss < 6; ss++)
                 if (ow + ss < a.Wo)
                     __builtin_amdgcn_raw_buffer_store_b16(
-                        __builtin_bit_cast(uint16_t, to_f16(out[rr][ss])), yrs,
-                        ybase + 2 * (rr * a.Wo + ss), 0, 0);
+                        __builtin_bit_cast(uint16_t, epilogue(out[rr][ss], a.bias, k, a.relu)),
+                        yrs, ybase + 2 * (rr * a.Wo + ss), 0, 0);
         }
     }
 }
@@ -439,8 +441,11 @@ const char* fused_name(const FusedPlan& p) {
 
 hipError_t launch_fused(const uint16_t* x, const uint16_t* Uf, uint16_t* y, uint16_t* Ms,
                         unsigned* cnt, int B, int C, int K, int Cp, int H, int W, int pad,
-                        int nh, int nw, int Ho, int Wo, const FusedPlan& p, hipStream_t s) {
+                        int nh, int nw, int Ho, int Wo, const FusedPlan& p, hipStream_t s,
+                        Epilogue ep) {
     FusedArgs a;
+    a.bias = reinterpret_cast<const _Float16*>(ep.bias);
+    a.relu = ep.relu;
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
     a.xd = (int)(xp & 15);

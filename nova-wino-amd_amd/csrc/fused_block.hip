@@ -63,6 +63,8 @@ struct BlockArgs {
     int chan2;    // (2*H*W) mod 16: span-alignment step per channel
     int nkt, nks; // 16-row output tiles and 16-channel steps of the fragment-ordered U
     int y_pairs;  // 1: store output pairs as 4-byte words (even Wo, 4-byte aligned y)
+    const _Float16* bias;  // output epilogue (null: none)
+    int relu;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -279,8 +281,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 #pragma unroll
                 for (int s = 0; s < 6; s += 2) {
                     if (ow + s < a.Wo) {
-                        const unsigned lo = __builtin_bit_cast(uint16_t, to_f16(out[r][s]));
-                        const unsigned hi = __builtin_bit_cast(uint16_t, to_f16(out[r][s + 1]));
+                        const unsigned lo =
+                            __builtin_bit_cast(uint16_t, epilogue(out[r][s], a.bias, k, a.relu));
+                        const unsigned hi = __builtin_bit_cast(
+                            uint16_t, epilogue(out[r][s + 1], a.bias, k, a.relu));
                         __builtin_amdgcn_raw_buffer_store_b32(lo | (hi << 16), yrs, row + 2 * s, 0,
                                                               0);
                     }
@@ -290,7 +294,8 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 for (int s = 0; s < 6; s++)
                     if (ow + s < a.Wo)
                         __builtin_amdgcn_raw_buffer_store_b16(
-                            __builtin_bit_cast(uint16_t, to_f16(out[r][s])), yrs, row + 2 * s, 0, 0);
+                            __builtin_bit_cast(uint16_t, epilogue(out[r][s], a.bias, k, a.relu)),
+                            yrs, row + 2 * s, 0, 0);
             }
         }
     }
@@ -328,8 +333,10 @@ bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
 
 hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
-                              int Wo, const FusedBlockPlan& p, hipStream_t s) {
+                              int Wo, const FusedBlockPlan& p, hipStream_t s, Epilogue ep) {
     BlockArgs a;
+    a.bias = reinterpret_cast<const _Float16*>(ep.bias);
+    a.relu = ep.relu;
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
     a.xd = (int)(xp & 15);

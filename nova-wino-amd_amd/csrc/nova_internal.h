@@ -19,6 +19,13 @@ enum Status : int {
 
 void set_error(int code, const char* fmt, ...);
 
+// Fused output epilogue: optional per-output-channel fp16 bias (device
+// pointer, K values) and ReLU, applied where the output transform stores y.
+struct Epilogue {
+    const uint16_t* bias = nullptr;
+    int relu = 0;
+};
+
 // Minimal tiling used by the product path: ceil(Ho/6) x ceil(Wo/6) tiles.
 inline int tiles_min(int out) { return (out + 5) / 6; }
 
@@ -55,7 +62,7 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
 // Reads M[p*pstride + bp*ldm + k]; writes y[b][k][h][w] for h < Ho, w < Wo.
 hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K, int Ho,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
-                                   hipStream_t s);
+                                   hipStream_t s, Epilogue ep = Epilogue());
 
 // ---- Winograd-domain batched GEMM ------------------------------------------
 // For p in 0..63: M_p[bp][k] = sum_c U_p[k][c] * V_p[bp][c]  (fp32 accumulate,
@@ -83,7 +90,8 @@ bool fused_fits(int64_t x_elems, int64_t u_elems, int64_t y_elems);
 const char* fused_name(const FusedPlan& p);
 hipError_t launch_fused(const uint16_t* x, const uint16_t* U, uint16_t* y, uint16_t* Ms,
                         unsigned* cnt, int B, int C, int K, int Cp, int H, int W, int pad,
-                        int nh, int nw, int Ho, int Wo, const FusedPlan& p, hipStream_t s);
+                        int nh, int nw, int Ho, int Wo, const FusedPlan& p, hipStream_t s,
+                        Epilogue ep = Epilogue());
 
 // Block variant (16-tile runs x 64 output channels x all positions per
 // workgroup, no scratch): layers with few channels at batch > 1.
@@ -95,6 +103,7 @@ bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
                       FusedBlockPlan* p);
 hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
-                              int Wo, const FusedBlockPlan& p, hipStream_t s);
+                              int Wo, const FusedBlockPlan& p, hipStream_t s,
+                              Epilogue ep = Epilogue());
 
 }  // namespace nova

@@ -26,6 +26,17 @@ __device__ __forceinline__ _Float16 to_f16(float v) {
     return (_Float16)v;
 }
 
+// Output epilogue for channel k: the convolution value rounded to fp16, then
+// the reference's separate bias add (`y + bias.half()`: fp16 + fp16 summed in
+// fp32, rounded once) and an optional ReLU (negative values -> 0). bias is a
+// device array of K fp16 values, or null.
+__device__ __forceinline__ _Float16 epilogue(float v, const _Float16* bias, int k, int relu) {
+    _Float16 h = to_f16(v);
+    if (bias != nullptr) h = to_f16((float)h + (float)bias[k]);
+    if (relu && (float)h < 0.0f) h = (_Float16)0.0f;
+    return h;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
 // L2. This bijection maps the dispatch index L (0..N-1) to a work index such
 // that every XCD receives one contiguous range of work items, so spatial

@@ -333,7 +333,8 @@ struct OutGeom {
 template <int TW, int kVW>
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
-    int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes) {
+    int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
+    const _Float16* __restrict__ bias, int relu) {
     using G = OutGeom<TW>;
     __shared__ __align__(16) _Float16 sy[G::kKB * G::kPlane];
     const int nwb = (nw + TW - 1) / TW;
@@ -361,10 +362,11 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
         output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
                     out);
         _Float16* sp = sy + kk * G::kPlane + t * 6;
+        const int kb = k < K ? k : 0;
 #pragma unroll
         for (int r = 0; r < 6; r++)
 #pragma unroll
-            for (int s = 0; s < 6; s++) sp[r * G::kCols + s] = to_f16(out[r][s]);
+            for (int s = 0; s < 6; s++) sp[r * G::kCols + s] = epilogue(out[r][s], bias, kb, relu);
     }
     __syncthreads();
 
@@ -422,22 +424,24 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
 template <int TW>
 static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, _Float16* yh,
                           int K, int Ho, int Wo, int nh, int nw, int ldm, int64_t pstride,
-                          int kblocks, int64_t m_bytes, int64_t y_bytes) {
+                          int kblocks, int64_t m_bytes, int64_t y_bytes, const _Float16* bias,
+                          int relu) {
     const dim3 block(256);
     if (vw == 4)
-        output_transform_kernel<TW, 4><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm,
-                                                              pstride, kblocks, m_bytes, y_bytes);
+        output_transform_kernel<TW, 4><<<grid, block, 0, s>>>(
+            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu);
     else if (vw == 2)
-        output_transform_kernel<TW, 2><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm,
-                                                              pstride, kblocks, m_bytes, y_bytes);
+        output_transform_kernel<TW, 2><<<grid, block, 0, s>>>(
+            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu);
     else
-        output_transform_kernel<TW, 1><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm,
-                                                              pstride, kblocks, m_bytes, y_bytes);
+        output_transform_kernel<TW, 1><<<grid, block, 0, s>>>(
+            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu);
 }
 
 hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K, int Ho,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
-                                   hipStream_t s) {
+                                   hipStream_t s, Epilogue ep) {
+    const _Float16* bias = reinterpret_cast<const _Float16*>(ep.bias);
     const int tw = pick_tw((int64_t)B * nh, nw, K);
     const int kb = 256 / tw;
     const int kblocks = (K + kb - 1) / kb;
@@ -456,15 +460,15 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
     switch (tw) {
         case 2:
             launch_out_tw<2>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
-                             m_bytes, y_bytes);
+                             m_bytes, y_bytes, bias, ep.relu);
             break;
         case 4:
             launch_out_tw<4>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
-                             m_bytes, y_bytes);
+                             m_bytes, y_bytes, bias, ep.relu);
             break;
         default:
             launch_out_tw<8>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
-                             m_bytes, y_bytes);
+                             m_bytes, y_bytes, bias, ep.relu);
             break;
     }
     return hipGetLastError();

@@ -55,7 +55,7 @@ class _Handle:
     """Owns one library handle; destroyed with the Python object (at
     interpreter exit the process releases device memory itself)."""
 
-    __slots__ = ("h", "lib", "stream", "key")
+    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16")
 
     def __init__(self):
         self.lib = get_lib()
@@ -63,6 +63,26 @@ class _Handle:
         check("create")
         self.stream = 0
         self.key = None
+        self.bias_key = None
+        self.bias16 = None
+
+    def set_bias(self, bias):
+        """Fuse the bias add into the output transform: the library adds an
+        fp16 copy of ``bias`` with the rounding of the reference's separate
+        ``output + bias.half()``. The copy is kept here while kernels may
+        read it and rebuilt when the parameter changes."""
+        if bias is None:
+            if self.bias_key is not None:
+                self.lib.nova_set_epilogue(self.h, None, 0)
+                self.bias_key = None
+                self.bias16 = None
+            return
+        key = (id(bias), bias._version, bias.data_ptr(), bias.dtype)
+        if key != self.bias_key:
+            self.bias16 = bias.detach().to(torch.float16).contiguous()
+            self.lib.nova_set_epilogue(self.h, ptr(self.bias16), 0)
+            check("set_epilogue")
+            self.bias_key = key
 
     def set_stream(self, device):
         s = current_stream_ptr(device)
@@ -310,6 +330,7 @@ class NovaWinogradConv2d(nn.Module):
         nh, nw, H_out, W_out = self._ensure_workspace(B, H, W)
         hd = self._handle
         hd.set_stream(x.device)
+        hd.set_bias(bias)
         output = torch.empty(B, self.out_channels, H_out, W_out, dtype=torch.float16,
                              device=x.device)
         V, M = self._V_gemm, self._M_gemm
@@ -320,8 +341,6 @@ class NovaWinogradConv2d(nn.Module):
             B, H, W, self.padding, nh, nw,
         )
         check("forward")
-        if bias is not None:
-            output = output + bias.half().view(1, -1, 1, 1)
         return output
 
     def forward(self, x):

@@ -53,6 +53,7 @@ _SIGNATURES = {
     "nova_get_last_error_message": (ctypes.c_char_p, []),
     "nova_set_stream": (None, [_vp, _vp]),
     "nova_set_path": (None, [_vp, _i]),
+    "nova_set_epilogue": (None, [_vp, _vp, _i]),
     "nova_get_last_path": (_i, [_vp]),
     "nova_workspace_bytes": (ctypes.c_longlong, [_vp, _i, _i, _i, _i]),
     "nova_profile_enable": (None, [_vp, _i]),
@@ -148,7 +149,7 @@ def compute_tiling(H, W, pad):
     return nh.value, nw.value, H_out.value, W_out.value
 
 
-def nova_forward(input_fp16, weight_fp32, padding=1):
+def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False):
     """Functional API: NOVA Winograd F(6,3) forward pass
     (/root/reference/nova_winograd/ops.py:147-176).
 
@@ -156,6 +157,11 @@ def nova_forward(input_fp16, weight_fp32, padding=1):
         input_fp16:  [B, C, H, W] float16 tensor on GPU.
         weight_fp32: [K, C, 3, 3] float32 tensor on GPU.
         padding:     Convolution padding (default 1).
+        bias:        optional [K] tensor on GPU, added in the output transform
+                     with the rounding of ``output + bias.half()`` (an
+                     extension: the reference has no bias here).
+        relu:        clamp negative outputs to zero in the same pass
+                     (extension).
 
     Returns:
         output: [B, K, H_out, W_out] float16 tensor on GPU.
@@ -178,11 +184,20 @@ def nova_forward(input_fp16, weight_fp32, padding=1):
     nh, nw, H_out, W_out = compute_tiling(H, W, padding)
     output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=input_fp16.device)
 
+    bias16 = None
+    if bias is not None:
+        require_gpu_tensor(bias, "bias")
+        assert bias.numel() == K
+        bias16 = bias.detach().to(torch.float16).contiguous()
     handle = _lib.nova_create()
     try:
         _lib.nova_set_stream(handle, current_stream_ptr(input_fp16.device))
         _lib.nova_set_weights(handle, ptr(weight_fp32), K, C)
         check("set_weights")
+        if bias16 is not None or relu:
+            _lib.nova_set_epilogue(handle, ptr(bias16) if bias16 is not None else None,
+                                   1 if relu else 0)
+            check("set_epilogue")
         _lib.nova_forward(handle, ptr(input_fp16), ptr(output), B, H, W, padding)
         check("forward")
     finally:
