@@ -4,7 +4,7 @@
 Classes:
     NovaWinogradConv2d           inference module: cached filter transform,
                                  weight versioning, workspace caching
-    NovaWinogradConv2dTrainable  HIP forward, fp32 backward
+    NovaWinogradConv2dTrainable  HIP forward; backward: grad input on the HIP path, grad weight fp32
     NovaWinogradConv2dCompilable ``torch.compile`` through the custom op
                                  ``torch.ops.nova.winograd_conv2d``
 
@@ -15,6 +15,7 @@ fallback (a CPU input raises).
 import atexit
 import math
 import threading
+import weakref
 
 import torch
 import torch.nn as nn
@@ -55,7 +56,7 @@ class _Handle:
     """Owns one library handle; destroyed with the Python object (at
     interpreter exit the process releases device memory itself)."""
 
-    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16")
+    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "w_ref")
 
     def __init__(self):
         self.lib = get_lib()
@@ -65,6 +66,19 @@ class _Handle:
         self.key = None
         self.bias_key = None
         self.bias16 = None
+        self.w_ref = None
+
+    def set_weights_cached(self, weight):
+        """Transform the filter unless this exact tensor object, unchanged
+        (same storage, same version), was the last one transformed. The
+        tensor is held by weak reference, so a freed temporary whose memory
+        is reused can never match."""
+        key = (weight.data_ptr(), weight._version, tuple(weight.shape), weight.dtype)
+        ref = self.w_ref
+        if ref is not None and ref[0]() is weight and ref[1] == key:
+            return
+        self.set_weights(weight)
+        self.w_ref = (weakref.ref(weight), key)
 
     def set_bias(self, bias):
         """Fuse the bias add into the output transform: the library adds an
@@ -118,11 +132,10 @@ _OP_HANDLES = {}  # device index -> _Handle
 
 
 def _op_handle(device):
-    """One persistent handle per device for the custom op. The op receives
-    bare tensors (possibly temporaries), so their identity cannot key a
-    filter-transform cache safely: the filter is re-transformed on every call,
-    as the reference's op does (it also creates and destroys a handle and
-    synchronises twice per call)."""
+    """One persistent handle per device for the custom op (the reference's op
+    creates and destroys a handle, transforms the filter and synchronises
+    twice per call). The filter transform is cached for the exact weight
+    tensor and version last seen (held by weak reference)."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     hd = _OP_HANDLES.get(idx)
     if hd is None:
@@ -133,6 +146,34 @@ def _op_handle(device):
 
 def _grad_input(go, weight, padding, dtype):
     return F.conv_transpose2d(go.float(), weight.float(), padding=padding).to(dtype)
+
+
+def _grad_input_nova(holder, go, weight, padding, dtype):
+    """dL/dx of a stride-1 3x3 convolution is itself a 3x3 convolution of
+    dL/dy with the filter flipped in both spatial axes and its channel axes
+    swapped, at padding 2 - padding -- so it runs on the NOVA forward path
+    (fp16, the same tolerance class as the forward). Padding above 2 has no
+    such form and falls back to PyTorch's fp32 transposed convolution."""
+    pb = 2 - padding
+    if pb < 0:
+        return _grad_input(go, weight, padding, dtype)
+    hd = getattr(holder, "_bwd_handle", None)
+    if hd is None:
+        hd = _Handle()
+        holder._bwd_handle = hd
+    hd.set_stream(go.device)
+    key = (weight.data_ptr(), weight._version, tuple(weight.shape), weight.dtype)
+    if hd.key != key:
+        hd.set_weights(weight.detach().flip(2, 3).transpose(0, 1))
+        hd.key = key
+    g16 = go.to(torch.float16).contiguous()
+    B, K, Ho, Wo = g16.shape
+    C = weight.shape[1]
+    gi = torch.empty(B, C, Ho + 2 * pb - 2, Wo + 2 * pb - 2, dtype=torch.float16,
+                     device=go.device)
+    hd.lib.nova_forward(hd.h, ptr(g16), ptr(gi), B, Ho, Wo, pb)
+    check("backward (grad input)")
+    return gi.to(dtype)
 
 
 def _grad_weight(inp, go, weight, padding):
@@ -164,7 +205,7 @@ def _register_custom_op():
         with _op_lock:
             hd = _op_handle(x.device)
             hd.set_stream(x.device)
-            hd.set_weights(w)
+            hd.set_weights_cached(weight)
             hd.lib.nova_forward(hd.h, ptr(x), ptr(output), B, H, W, padding)
             check("forward")
         return output
@@ -196,12 +237,14 @@ def _register_custom_op():
 # ─────────────────────────────────────────────────────────────────────────
 
 class NovaWinogradFunction(torch.autograd.Function):
-    """HIP forward, fp32 backward."""
+    """HIP forward; backward: grad input through the HIP forward (flipped
+    filter), grad weight and bias in fp32."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, padding, handle_holder):
         ctx.save_for_backward(input, weight, bias)
         ctx.padding = padding
+        ctx.holder = handle_holder
         x = input.half().contiguous() if input.dtype != torch.float16 else input.contiguous()
         return handle_holder._run(x, bias)
 
@@ -212,7 +255,7 @@ class NovaWinogradFunction(torch.autograd.Function):
         grad_input = grad_weight = grad_bias = None
         go = grad_output.contiguous()
         if ctx.needs_input_grad[0]:
-            grad_input = _grad_input(go, weight, padding, input.dtype)
+            grad_input = _grad_input_nova(ctx.holder, go, weight, padding, input.dtype)
         if ctx.needs_input_grad[1]:
             grad_weight = _grad_weight(input, go, weight, padding)
         if bias is not None and ctx.needs_input_grad[2]:
@@ -381,7 +424,8 @@ class NovaWinogradConv2d(nn.Module):
 # ─────────────────────────────────────────────────────────────────────────
 
 class NovaWinogradConv2dTrainable(NovaWinogradConv2d):
-    """NOVA conv with backward support: HIP forward, fp32 backward."""
+    """NOVA conv with backward support: HIP forward and grad input, fp32 grad
+    weight."""
 
     def forward(self, x):
         if not x.is_contiguous():
