@@ -285,6 +285,99 @@ def cpu_baseline(layers_spec, budget_s, threads):
     }
 
 
+EXTRA_LAYERS = [
+    # (name, B, C, K, H): BASELINE config 3 (B=128), 4 (SD-1.5, B=2), 5 (SDXL B=1,
+    # DenseNet-161 bottleneck 192->48 B=1)
+    ("r50_conv2_x", 128, 64, 64, 56), ("r50_conv3_x", 128, 128, 128, 28),
+    ("r50_conv4_x", 128, 256, 256, 14), ("r50_conv5_x", 128, 512, 512, 7),
+    ("sd15_320@64", 2, 320, 320, 64), ("sd15_640@32", 2, 640, 640, 32),
+    ("sd15_1280@16", 2, 1280, 1280, 16), ("sd15_1280@8", 2, 1280, 1280, 8),
+    ("sd15_320to640@32", 2, 320, 640, 32), ("sd15_640to1280@16", 2, 640, 1280, 16),
+    ("sd15_1280to640@32", 2, 1280, 640, 32), ("sd15_640to320@64", 2, 640, 320, 64),
+    ("sdxl_320@128", 1, 320, 320, 128), ("sdxl_640@64", 1, 640, 640, 64),
+    ("sdxl_1280@32", 1, 1280, 1280, 32),
+    ("dn161_192to48@56", 1, 192, 48, 56), ("dn161_192to48@28", 1, 192, 48, 28),
+    ("dn161_192to48@14", 1, 192, 48, 14), ("dn161_192to48@7", 1, 192, 48, 7),
+]
+
+
+def extra_measurements(runs, lib, torch, nn, nw, reps):
+    """Per-layer NOVA vs MIOpen on the other BASELINE configs, the full
+    random-init ResNet-50 forward with and without surgery, and cold-cache
+    times of the headline layers (a 512 MiB write between reps evicts the
+    256 MB Infinity Cache and the L2s)."""
+    dev = torch.device("cuda:0")
+    path_names = {1: "3-pass", 2: "fused_rows", 3: "fused_block"}
+    out = {"layers": []}
+    for name, B, C, K, H in EXTRA_LAYERS:
+        torch.manual_seed(0)
+        x = torch.randn(B, C, H, H, device=dev).half()
+        w = torch.empty(K, C, 3, 3)
+        nn.init.kaiming_normal_(w, mode="fan_in", nonlinearity="relu")
+        mod = nw.NovaWinogradConv2d(C, K, kernel_size=3, padding=1).to(dev)
+        mio = nn.Conv2d(C, K, 3, padding=1, bias=False).to(dev).half()
+        with torch.no_grad():
+            mod.weight.copy_(w.to(dev))
+            mio.weight.copy_(w.half().to(dev))
+            mod(x)
+            mio(x)
+            tn = time_region(lambda: mod(x), reps, torch)
+            tm = time_region(lambda: mio(x), reps, torch)
+        f = direct_flops(B, C, K, H, H)
+        rec = {"layer": name, "B": B, "C": C, "K": K, "H": H,
+               "path": path_names.get(lib.nova_get_last_path(mod._handle.h), "?"),
+               "nova_ms": round(tn, 5), "miopen_ms": round(tm, 5),
+               "nova_tflops": round(f / (tn * 1e-3) / 1e12, 2),
+               "speedup_vs_miopen": round(tm / tn, 3),
+               "roofline_frac": round(layer_roofline_us(B, C, K, H) / (tn * 1e3), 4)}
+        out["layers"].append(rec)
+        log(f"{name:18s} B={B:<3d} {rec['path']:11s} nova {tn*1e3:9.2f} us  miopen "
+            f"{tm*1e3:9.2f} us")
+        del x, mod, mio
+    # full ResNet-50 (BASELINE config 3), eager, MIOpen fp16 vs after surgery
+    import copy
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from resnet50 import ResNet50
+
+    out["resnet50"] = []
+    for B in (1, 32):
+        torch.manual_seed(0)
+        m16 = ResNet50().eval().to(dev).half()
+        nova = copy.deepcopy(m16)
+        nw.replace_conv2d_with_nova(nova, verbose=False)
+        x = torch.randn(B, 3, 224, 224, device=dev).half()
+        with torch.no_grad():
+            m16(x)
+            nova(x)
+            t16 = time_region(lambda: m16(x), 20, torch)
+            tn = time_region(lambda: nova(x), 20, torch)
+        out["resnet50"].append({"B": B, "miopen_ms": round(t16, 4), "nova_ms": round(tn, 4),
+                                "speedup": round(t16 / tn, 3)})
+        log(f"resnet50 B={B:<3d} model forward: miopen {t16:8.3f} ms  nova {tn:8.3f} ms")
+        del m16, nova, x
+    # cold-cache times of the headline layers
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    out["cold"] = []
+    for r in runs:
+        ts = []
+        with torch.no_grad():
+            for _ in range(20):
+                flush.fill_(1)
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                r["mod"](r["x"])
+                e1.record()
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+        tc = sorted(ts)[len(ts) // 2]
+        troof = layer_roofline_us(r["B"], r["C"], r["K"], r["H"])
+        out["cold"].append({"layer": r["name"], "B": r["B"], "nova_cold_ms": round(tc, 5),
+                            "roofline_frac_cold": round(troof / (tc * 1e3), 4)})
+    del flush
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -297,6 +390,9 @@ def main():
     ap.add_argument("--no-miopen", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--details", default="", help="write the full per-layer report here")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the extra measurements (BASELINE configs 3-5 layers, full "
+                         "ResNet-50, cold-cache layer times)")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="short run for rocprofv3 --pmc passes (copy calibration + forwards)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -468,6 +564,10 @@ def main():
             + (f" miopen {r['miopen_graph_ms']*1e3:7.2f} us" if r.get("miopen_graph_ms") else "")
             + f"  roofline {troof:6.2f} us")
 
+    extra = None
+    if not args.no_extra:
+        extra = extra_measurements(runs, lib, torch, nn, nw, 50)
+
     cpu = None
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
@@ -500,9 +600,11 @@ def main():
         "cpu_baseline": cpu,
         "layers": layers_out,
     }
+    if extra is not None:
+        out["resnet50_model"] = extra["resnet50"]
     if args.details:
         with open(args.details, "w") as f:
-            json.dump({"bench": out, "kernels": kernels}, f, indent=2)
+            json.dump({"bench": out, "kernels": kernels, "extra": extra}, f, indent=2)
     print(json.dumps(out), flush=True)
 
 
