@@ -150,13 +150,15 @@ NOVA_KERNELS = ["input_transform_kernel", "output_transform_kernel",
 
 
 def _name_keys(name):
-    """The kernel's name as it appears demangled and Itanium-mangled (int
-    template arguments only), for matching rocprofv3 records."""
+    """Prefixes of the kernel's name as it appears demangled and
+    Itanium-mangled (int template arguments only), for matching rocprofv3
+    records; trailing template arguments the library's short name leaves
+    out (tuning depths) still match."""
     if "<" not in name:
         return [name]
     base, args = name.split("<", 1)
     args = [a.strip() for a in args.rstrip(">").split(",")]
-    return [name, base + "I" + "".join(f"Li{a}E" for a in args) + "E"]
+    return [name.rstrip(">"), base + "I" + "".join(f"Li{a}E" for a in args)]
 
 
 def traffic_from(fetch_dir, write_dir, out_path):

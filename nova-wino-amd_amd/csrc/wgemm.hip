@@ -15,6 +15,7 @@
 // 8-channel groups. No atomics, no split-K: results are deterministic.
 // Byte offsets are 32-bit: U, V and M must each stay below 2 GB.
 #include "nova_internal.h"
+#include "nova_tile_math.h"
 
 namespace nova {
 
@@ -170,9 +171,15 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wk = wave % WK, wb = wave / WK;
-    const int p = blockIdx.z;
-    const int k0 = blockIdx.y * TK;
-    const int n0 = blockIdx.x * TB;
+    // One-dimensional grid, XCD-aware: every XCD takes a contiguous run of
+    // (position, k-tile, bp-tile) items with the bp tile fastest, so all
+    // tiles of a position meet in one L2 and U_p, V_p leave HBM once.
+    const int nbt = (BP + TB - 1) / TB, nkt = (K + TK - 1) / TK;
+    const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int p = item / (nbt * nkt);
+    const int rem = item - p * (nbt * nkt);
+    const int k0 = (rem / nbt) * TK;
+    const int n0 = (rem % nbt) * TB;
     const int r16 = lane & 15, g = lane >> 4;
 
     const __amdgpu_buffer_rsrc_t urs = make_rsrc(U, 2 * (int64_t)64 * K * Cp);
@@ -297,8 +304,8 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
 template <int TK, int TB, int WK, int WB, int PF>
 static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                              int BP, hipStream_t s) {
-    dim3 grid((unsigned)((BP + TB - 1) / TB), (unsigned)((K + TK - 1) / TK), 64);
-    wgemm_lds_kernel<TK, TB, WK, WB, PF><<<grid, dim3(256), 0, s>>>(
+    const unsigned grid = 64u * (unsigned)((BP + TB - 1) / TB) * (unsigned)((K + TK - 1) / TK);
+    wgemm_lds_kernel<TK, TB, WK, WB, PF><<<dim3(grid), dim3(256), 0, s>>>(
         reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
         reinterpret_cast<_Float16*>(M), K, Cp, BP);
     return hipGetLastError();
