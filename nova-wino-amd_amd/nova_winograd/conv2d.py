@@ -22,6 +22,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from nova_winograd.ops import (
+    _raw_stream,
     check,
     compute_tiling,
     current_stream_ptr,
@@ -303,6 +304,7 @@ class NovaWinogradConv2d(nn.Module):
         self._M_gemm = None
         self._last_config = None
         self._tiling = None
+        self._state = None
 
     # -- caches -------------------------------------------------------------
     def invalidate_weight_cache(self):
@@ -310,6 +312,7 @@ class NovaWinogradConv2d(nn.Module):
         after writing the weights through ``.data``, which PyTorch does not
         version)."""
         self._weight_version = -1
+        self._state = None
         if self._handle is not None:
             self._handle.key = None
 
@@ -318,6 +321,7 @@ class NovaWinogradConv2d(nn.Module):
         self.invalidate_weight_cache()
         self._V_gemm = self._M_gemm = None
         self._last_config = None
+        self._state = None
         return out
 
     def _load_from_state_dict(self, *args, **kwargs):
@@ -372,7 +376,6 @@ class NovaWinogradConv2d(nn.Module):
         self._ensure_handle()
         nh, nw, H_out, W_out = self._ensure_workspace(B, H, W)
         hd = self._handle
-        hd.set_stream(x.device)
         hd.set_bias(bias)
         output = torch.empty(B, self.out_channels, H_out, W_out, dtype=torch.float16,
                              device=x.device)
@@ -387,10 +390,50 @@ class NovaWinogradConv2d(nn.Module):
         return output
 
     def forward(self, x):
+        # Fast path: the same input shape, weight and bias objects at the same
+        # versions, and the same current stream as the previous call -- only
+        # the output allocation and the launch remain.
+        st = self._state
+        if st is not None:
+            w, b = self.weight, self.bias
+            if (x.shape == st[0] and w is st[1] and w._version == st[2]
+                    and w.data_ptr() == st[13] and b is st[3]
+                    and (b is None or (b._version, b.data_ptr()) == st[4])
+                    and x.dtype == torch.float16
+                    and x.is_contiguous() and x.device == st[5]
+                    and _raw_stream(st[6]) == st[7]):
+                out = torch.empty(st[8], dtype=torch.float16, device=st[5])
+                st[9](st[10], x.data_ptr(), out.data_ptr(), *st[11])
+                if st[12]():
+                    check("forward")
+                return out
         assert x.dtype == torch.float16, f"Input must be float16, got {x.dtype}"
         assert x.is_contiguous(), "Input must be contiguous"
         assert x.dim() == 4 and x.shape[1] == self.in_channels
-        return self._run(x, self.bias)
+        out = self._run(x, self.bias)
+        self._remember(x)
+        return out
+
+    def _remember(self, x):
+        """Record what the fast path of ``forward`` checks and replays. The
+        weight and bias objects are held, so their identities cannot be
+        reused by other tensors while the record exists."""
+        hd = self._handle
+        B, C, H, W = x.shape
+        nh, nw, H_out, W_out = self._tiling
+        V, M = self._V_gemm, self._M_gemm
+        w, b = self.weight, self.bias
+        idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
+        self._state = (
+            x.shape, w, w._version, b, None if b is None else (b._version, b.data_ptr()),
+            x.device, idx,
+            hd.stream, (B, self.out_channels, H_out, W_out), hd.lib.nova_forward_workspace,
+            hd.h,
+            (V.data_ptr() if V is not None else None, M.data_ptr() if M is not None else None,
+             B, H, W, self.padding, nh, nw),
+            hd.lib.nova_get_last_error,
+            w.data_ptr(),
+        )
 
     @classmethod
     def from_conv2d(cls, conv):

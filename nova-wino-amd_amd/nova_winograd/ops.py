@@ -133,8 +133,13 @@ def require_gpu_tensor(t, name="input"):
         )
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream  # device index -> hipStream_t (int)
+
+
 def current_stream_ptr(device):
-    return torch.cuda.current_stream(device).cuda_stream
+    """Raw hipStream_t of torch's current stream on ``device`` (an int)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _raw_stream(idx)
 
 
 def compute_tiling(H, W, pad):

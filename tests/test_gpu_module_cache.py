@@ -1,0 +1,75 @@
+"""The module's cached forward: after a first call, repeated calls with the
+same input shape, weight and bias (same objects, same versions, same storage)
+on the same stream only allocate the output and launch. Every change that
+the cache keys on must send the next call back through the full path: an
+in-place weight update, a weight re-bound through ``.data``, a new bias, a
+new input shape and a different current stream. Each result is compared
+bitwise with a freshly built module holding the same parameters.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _fresh(conv):
+    from nova_winograd import NovaWinogradConv2d
+
+    ref = NovaWinogradConv2d(conv.in_channels, conv.out_channels, padding=conv.padding,
+                             bias=conv.bias is not None).to(DEV)
+    with torch.no_grad():
+        ref.weight.copy_(conv.weight)
+        if conv.bias is not None:
+            ref.bias.copy_(conv.bias)
+    return ref
+
+
+def test_cached_forward_invalidation():
+    from nova_winograd import NovaWinogradConv2d
+
+    print("[module cache]", flush=True)
+    torch.manual_seed(11)
+    conv = NovaWinogradConv2d(16, 24, kernel_size=3, padding=1, bias=True).to(DEV)
+    with torch.no_grad():
+        conv.bias.copy_(torch.randn(24))
+    x = torch.randn(2, 16, 12, 12, device=DEV).half()
+    with torch.no_grad():
+        y0 = conv(x)
+        assert conv._state is not None  # the next call takes the cached path
+        y1 = conv(x)
+        assert torch.equal(y0, y1)
+        assert torch.equal(y1, _fresh(conv)(x))
+
+        conv.weight.mul_(0.5)  # in place: version bump
+        y2 = conv(x)
+        assert torch.equal(y2, _fresh(conv)(x))
+        assert not torch.equal(y2, y1)
+
+        conv.weight.data = torch.randn(24, 16, 3, 3, device=DEV)  # new storage, no bump
+        y3 = conv(x)
+        assert torch.equal(y3, _fresh(conv)(x))
+
+        conv.bias = torch.nn.Parameter(torch.randn(24, device=DEV))  # new bias object
+        y4 = conv(x)
+        assert torch.equal(y4, _fresh(conv)(x))
+
+        x2 = torch.randn(1, 16, 20, 18, device=DEV).half()  # new shape
+        y5 = conv(x2)
+        assert y5.shape == (1, 24, 20, 18)
+        assert torch.equal(y5, _fresh(conv)(x2))
+
+        s = torch.cuda.Stream()  # new current stream
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            y6 = conv(x)
+            y6b = conv(x)  # cached path on the side stream
+        s.synchronize()
+        torch.cuda.current_stream().wait_stream(s)
+        assert torch.equal(y6, y4)
+        assert torch.equal(y6b, y4)
+        y7 = conv(x)  # back on the default stream
+        assert torch.equal(y7, y4)
+    torch.cuda.synchronize()

@@ -82,9 +82,12 @@ def test_filter_transform_bitexact(oracle, K, C):
     assert_same_bits(_u16(U), ref, f"U K={K} C={C}")
 
 
+# Small problems run the lane-parallel kernel, large ones (the last two: a
+# tile-block grid of 256 workgroups or more) the tile-block kernel.
 INPUT_CASES = [
     (1, 64, 56, 56, 1), (2, 3, 13, 13, 1), (1, 128, 28, 28, 1), (1, 16, 7, 7, 1),
     (1, 24, 14, 9, 0), (1, 8, 11, 11, 2), (3, 72, 20, 17, 1), (1, 130, 5, 5, 1),
+    (8, 64, 56, 56, 1), (12, 130, 27, 29, 1),
 ]
 
 
@@ -101,7 +104,8 @@ def test_input_transform_bitexact(oracle, B, C, H, W, pad):
     assert_same_bits(_u16(V), ref, "V")
 
 
-OUTPUT_CASES = [(1, 64, 56, 56), (2, 48, 14, 14), (1, 130, 7, 9), (3, 8, 13, 11), (1, 16, 1, 1)]
+OUTPUT_CASES = [(1, 64, 56, 56), (2, 48, 14, 14), (1, 130, 7, 9), (3, 8, 13, 11), (1, 16, 1, 1),
+                (8, 64, 56, 56), (12, 130, 27, 29)]
 
 
 @pytest.mark.parametrize("B,K,Ho,Wo", OUTPUT_CASES)
