@@ -150,9 +150,10 @@ struct InGeom {
     // Channel pitch 8 x odd: lanes over consecutive channels then hit at most
     // two channels per LDS bank (staging writes are 8-byte halves).
     static constexpr int kCP = 8 * kRP + 8;
-    static constexpr int kPieces = kCB * 8 * kNJ / 256;            // loads per thread
+    static constexpr int kUnits = kCB * 8 / 256;                    // (channel, row) spans per
+                                                                   // thread
     static constexpr int kBytes = kCB * kCP;
-    static_assert(kCB * 8 * kNJ % 256 == 0, "staging pieces must tile the workgroup");
+    static_assert(kCB * 8 % 256 == 0, "staged spans must tile the workgroup");
     static_assert((kCP / 8) % 2 == 1, "channel pitch must be an odd number of 8-byte units");
     __device__ static int base(int c) { return c * kCP; }
 };
@@ -182,30 +183,40 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x_al, x_bytes);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
 
-    // ---- staging: piece e = (channel c, row r, 16-byte column j16) ----
+    // ---- staging: thread = row r (tid % 8) of channels tid / 8 + 32u ----
+    // Each thread copies whole row spans (kNJ 16-byte loads at immediate
+    // offsets); its spans are 32 channels apart, a constant byte step, and
+    // their LDS destinations are immediate offsets. The whole offset stays in
+    // the range-checked vector offset, so span bytes past the end of x read
+    // zero.
     {
         typedef unsigned u4 __attribute__((ext_vector_type(4)));
-        u4 val[G::kPieces];
-        int lo[G::kPieces];
-#pragma unroll
-        for (int u = 0; u < G::kPieces; u++) {
-            const int e = threadIdx.x + u * 256;
-            const int j16 = e % G::kNJ;
-            const int rest = e / G::kNJ;
-            const int r = rest % 8, c = rest / 8;
-            const int h = h0 + r;
-            const bool ok = h >= 0 && h < H && c0 + c < C;
-            const int o = xbase + 2 * (c * HW + h * W);
-            val[u] = ok ? __builtin_amdgcn_raw_buffer_load_b128(xrs, (o & ~15) + 16 * j16, 0, 0)
-                        : u4{0u, 0u, 0u, 0u};
-            lo[u] = G::base(c) + r * G::kRP + 16 * j16;
-        }
         typedef unsigned u2 __attribute__((ext_vector_type(2)));
+        const int r = threadIdx.x & 7, c = threadIdx.x >> 3;
+        const int h = h0 + r;
+        const bool row_ok = h >= 0 && h < H;
+        // 64*HW bytes per 32 channels is a multiple of 16: every span of this
+        // thread starts at the same offset within its 16-byte granule
+        const int ga = (xbase + 2 * (c * HW + h * W)) & ~15;
+        unsigned char* dst = sx + G::base(c) + r * G::kRP;
+        u4 val[G::kUnits][G::kNJ];
 #pragma unroll
-        for (int u = 0; u < G::kPieces; u++) {
-            *reinterpret_cast<u2*>(sx + lo[u]) = u2{val[u][0], val[u][1]};
-            *reinterpret_cast<u2*>(sx + lo[u] + 8) = u2{val[u][2], val[u][3]};
+        for (int u = 0; u < G::kUnits; u++) {
+            // rows outside the image and channels past C: out-of-range offset,
+            // the loads return zeros
+            const int vo = (row_ok && c0 + c + 32 * u < C) ? ga + 64 * u * HW : kOob;
+#pragma unroll
+            for (int q = 0; q < G::kNJ; q++)
+                val[u][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, vo + 16 * q, 0, 0);
         }
+#pragma unroll
+        for (int u = 0; u < G::kUnits; u++)
+#pragma unroll
+            for (int q = 0; q < G::kNJ; q++) {
+                unsigned char* d = dst + 32 * u * G::kCP + 16 * q;
+                *reinterpret_cast<u2*>(d) = u2{val[u][q][0], val[u][q][1]};
+                *reinterpret_cast<u2*>(d + 8) = u2{val[u][q][2], val[u][q][3]};
+            }
     }
     __syncthreads();
 
@@ -222,6 +233,12 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
         const int w = w0 + 6 * t + j;
         cmask |= (w >= 0 && w < W) ? (1u << j) : 0u;
     }
+    // column mask as four dword masks over the packed halves
+    unsigned dm[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        dm[q] = (((cmask >> (2 * q)) & 1u) ? 0xffffu : 0u) |
+                (((cmask >> (2 * q + 1)) & 1u) ? 0xffff0000u : 0u);
     // Row i of the patch: 8 halves at byte sb = rho + 12t of its span. Read
     // the five aligned dwords from floor4(sb) and shift each output dword by
     // (sb & 3) bytes (0 or 2) with v_alignbyte: aligned LDS reads only.
@@ -239,11 +256,19 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
         for (int q = 0; q < 4; q++)
             d4[i][q] = __builtin_amdgcn_alignbyte(w5[q + 1], w5[q], (unsigned)(sb & 3));
     }
+    // edge tiles: zero the columns outside the image (zero padding, or bytes of
+    // the neighbouring row that the aligned span picked up)
+    if (cmask != 0xffu) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) d4[i][q] &= dm[q];
+    }
     input_tile_rows(
         [&](int i, int j) {
             const unsigned pair = d4[i][j >> 1];
             const unsigned short bits = (unsigned short)((j & 1) ? (pair >> 16) : (pair & 0xffffu));
-            return ((cmask >> j) & 1u) ? (float)__builtin_bit_cast(_Float16, bits) : 0.0f;
+            return (float)__builtin_bit_cast(_Float16, bits);
         },
         [&](int r, int s, float v) {
             const int p = r * 8 + s;
