@@ -108,6 +108,13 @@ NOVA_API int nova_get_last_error(void);
 /* Message for the calling thread's most recent error ("" if none). */
 NOVA_API const char* nova_get_last_error_message(void);
 
+/* No counterpart in the reference: nova_set_weights for fp16 w[K][C][3][3],
+ * so that a module converted with .half() passes its weights without an fp32
+ * copy (the reference reads such weights as fp32 bits). Each weight widens to
+ * fp32 exactly: the transform equals nova_set_weights on the fp32 copy, bit
+ * for bit. */
+NOVA_API void nova_set_weights_f16(nova_handle_t h, const void* d_weight_f16, int K, int C);
+
 /* Stream for the handle's subsequent work (a hipStream_t; NULL = null stream). */
 NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
 
@@ -123,6 +130,13 @@ NOVA_API void nova_set_path(nova_handle_t h, int path);
  * separate elementwise op after the convolution
  * (/root/reference/nova_winograd/conv2d.py:240-241). */
 NOVA_API void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu);
+/* Residual of every subsequent forward on the handle: an fp16 tensor with the
+ * output's shape and layout [B][K][Ho][Wo], added after the bias and before
+ * the ReLU (each add rounded to fp16, as separate `y + bias.half()` and
+ * `y + residual` ops); NULL: none. It is a per-call operand: set it before
+ * each forward that uses it and clear it after. No counterpart in the
+ * reference (a residual there is a separate elementwise op). */
+NOVA_API void nova_set_residual(nova_handle_t h, const void* d_residual_f16);
 /* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused
  * (position rows), 3 = fused (tile blocks). */
 NOVA_API int nova_get_last_path(nova_handle_t h);

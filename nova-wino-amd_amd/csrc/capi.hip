@@ -235,7 +235,7 @@ int choose_path(const Handle* Hd, const Shape& s) {
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
 bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* V,
-                    uint16_t* M, bool remember) {
+                    uint16_t* M, bool remember, const Epilogue& ep) {
     Profiler& pf = Hd->prof;
     const hipStream_t st = Hd->stream;
     const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
@@ -245,7 +245,6 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
                                       (int64_t)Cp * s.BP, st);
     };
     auto gm = [=]() { return launch_wgemm(U, V, M, K, Cp, (int)s.BP, st); };
-    const Epilogue ep = Hd->ep;
     auto out = [=]() {
         return launch_output_transform(M, y, s.B, K, s.Ho, s.Wo, s.nh, s.nw, K,
                                        (int64_t)K * s.BP, st, ep);
@@ -329,6 +328,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         s.BP = (int64_t)s.B * s.nh * s.nw;
         const uint16_t* xx = static_cast<const uint16_t*>(x) + b0 * x_img;
         uint16_t* yy = static_cast<uint16_t*>(y) + b0 * y_img;
+        Epilogue ep = Hd->ep;  // the residual follows the output's sub-batch
+        if (ep.residual) ep.residual += b0 * y_img;
         if (path == 3) {
             const hipStream_t st = Hd->stream;
             const uint16_t* U = Hd->Uf;
@@ -338,7 +339,6 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
                 return;
             }
-            const Epilogue ep = Hd->ep;
             auto fz = [=]() {
                 return launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
                                           s.Ho, s.Wo, bp, st, ep);
@@ -364,7 +364,6 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 return;
             uint16_t* Ms = static_cast<uint16_t*>(Hd->ws);
             unsigned* cnt = Hd->cnt;
-            const Epilogue ep = Hd->ep;
             auto fz = [=]() {
                 return launch_fused(xx, U, yy, Ms, cnt, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh,
                                     s.nw, s.Ho, s.Wo, fp, st, ep);
@@ -377,7 +376,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             const size_t e0 = pf.mark(st);
             if (!hip_ok(fz(), "fused kernel")) return;
             pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
-        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0)) {
+        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0, ep)) {
             return;
         }
     }
@@ -409,12 +408,16 @@ void nova_destroy(nova_handle_t h) {
     delete H;
 }
 
-void nova_set_weights(nova_handle_t h, const void* d_weight, int K, int C) {
-    Handle* H = as_handle(h, "nova_set_weights");
+}  // extern "C"
+
+namespace {
+
+void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool w_f16,
+                      const char* fn) {
+    Handle* H = as_handle(h, fn);
     if (!H) return;
     if (d_weight == nullptr || K < 1 || C < 1) {
-        set_error(kErrInvalidArgument, "nova_set_weights: bad arguments (w=%p K=%d C=%d)",
-                  d_weight, K, C);
+        set_error(kErrInvalidArgument, "%s: bad arguments (w=%p K=%d C=%d)", fn, d_weight, K, C);
         return;
     }
     const int Cp = pad8(C);
@@ -447,10 +450,21 @@ void nova_set_weights(nova_handle_t h, const void* d_weight, int K, int C) {
     H->K = K;
     H->C = C;
     H->Cp = Cp;
-    H->ready = hip_ok(launch_filter_transform_gemm(static_cast<const float*>(d_weight), H->U, K,
-                                                   C, Cp, H->stream),
+    H->ready = hip_ok(launch_filter_transform_gemm(d_weight, w_f16, H->U, K, C, Cp, H->stream),
                       "filter transform") &&
                hip_ok(launch_u_frag(H->U, H->Uf, K, Cp, H->stream), "filter fragment order");
+}
+
+}  // namespace
+
+extern "C" {
+
+void nova_set_weights(nova_handle_t h, const void* d_weight, int K, int C) {
+    set_weights_impl(h, d_weight, K, C, false, "nova_set_weights");
+}
+
+void nova_set_weights_f16(nova_handle_t h, const void* d_weight_f16, int K, int C) {
+    set_weights_impl(h, d_weight_f16, K, C, true, "nova_set_weights_f16");
 }
 
 void nova_forward(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
@@ -600,6 +614,12 @@ void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu) {
     }
     H->ep.bias = static_cast<const uint16_t*>(d_bias_f16);
     H->ep.relu = relu;
+}
+
+void nova_set_residual(nova_handle_t h, const void* d_residual_f16) {
+    Handle* H = as_handle(h, "nova_set_residual");
+    if (!H) return;
+    H->ep.residual = static_cast<const uint16_t*>(d_residual_f16);
 }
 
 int nova_get_last_path(nova_handle_t h) {

@@ -65,6 +65,7 @@ struct FusedArgs {
     int nkt, nks;        // 16-row tiles / 16-channel steps of the fragment-ordered U
     const _Float16* bias;  // output epilogue (null: none)
     int relu;
+    const _Float16* residual;  // added after the bias, y's layout (null: none)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -353,15 +354,24 @@ __global__ __launch_bounds__(kFThreads, 1) void fused_kernel(FusedArgs a) {
         output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
         const int oh = th * 6, ow = tw * 6;
         const int ybase = 2 * (((b * a.K + k) * a.Ho + oh) * a.Wo + ow);
+        const __amdgpu_buffer_rsrc_t rrs = rsrc(a.residual, a.residual ? a.y_bytes : 0);
 #pragma unroll
         for (int rr = 0; rr < 6; rr++) {
             if (oh + rr >= a.Ho) break;
 #pragma unroll
             for (int ss = 0; ss < 6; ss++)
-                if (ow + ss < a.Wo)
-                    __builtin_amdgcn_raw_buffer_store_b16(
-                        __builtin_bit_cast(uint16_t, epilogue(out[rr][ss], a.bias, k, a.relu)),
-                        yrs, ybase + 2 * (rr * a.Wo + ss), 0, 0);
+                if (ow + ss < a.Wo) {
+                    const int off = ybase + 2 * (rr * a.Wo + ss);
+                    _Float16 v = epilogue(out[rr][ss], a.bias, k, a.residual ? 0 : a.relu);
+                    if (a.residual)
+                        v = add_residual(v,
+                                         __builtin_bit_cast(_Float16,
+                                                            __builtin_amdgcn_raw_buffer_load_b16(
+                                                                rrs, off, 0, 0)),
+                                         a.relu);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs, off,
+                                                          0, 0);
+                }
         }
     }
 }
@@ -446,6 +456,7 @@ hipError_t launch_fused(const uint16_t* x, const uint16_t* Uf, uint16_t* y, uint
     FusedArgs a;
     a.bias = reinterpret_cast<const _Float16*>(ep.bias);
     a.relu = ep.relu;
+    a.residual = reinterpret_cast<const _Float16*>(ep.residual);
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
     a.xd = (int)(xp & 15);

@@ -65,6 +65,7 @@ struct BlockArgs {
     int y_pairs;  // 1: store output pairs as 4-byte words (even Wo, 4-byte aligned y)
     const _Float16* bias;  // output epilogue (null: none)
     int relu;
+    const _Float16* residual;  // added after the bias, y's layout (null: none)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -261,6 +262,9 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 
     // ---- output transform: (kk, tile) pairs, tile = tid % 16 ----
     const bool pairs_w = a.y_pairs != 0;
+    const _Float16* res = a.residual;
+    const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
+    const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
     for (int e = tid; e < 64 * 16; e += kBT) {
         const int kk = e >> 4;
         const int k = k0 + kk;
@@ -282,20 +286,31 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 for (int s = 0; s < 6; s += 2) {
                     if (ow + s < a.Wo) {
                         const unsigned lo =
-                            __builtin_bit_cast(uint16_t, epilogue(out[r][s], a.bias, k, a.relu));
+                            __builtin_bit_cast(uint16_t, epilogue(out[r][s], a.bias, k, relu0));
                         const unsigned hi = __builtin_bit_cast(
-                            uint16_t, epilogue(out[r][s + 1], a.bias, k, a.relu));
-                        __builtin_amdgcn_raw_buffer_store_b32(lo | (hi << 16), yrs, row + 2 * s, 0,
-                                                              0);
+                            uint16_t, epilogue(out[r][s + 1], a.bias, k, relu0));
+                        unsigned v = lo | (hi << 16);
+                        if (res)
+                            v = add_residual2(
+                                v, __builtin_amdgcn_raw_buffer_load_b32(rrs, row + 2 * s, 0, 0),
+                                a.relu);
+                        __builtin_amdgcn_raw_buffer_store_b32(v, yrs, row + 2 * s, 0, 0);
                     }
                 }
             } else {
 #pragma unroll
                 for (int s = 0; s < 6; s++)
-                    if (ow + s < a.Wo)
-                        __builtin_amdgcn_raw_buffer_store_b16(
-                            __builtin_bit_cast(uint16_t, epilogue(out[r][s], a.bias, k, a.relu)),
-                            yrs, row + 2 * s, 0, 0);
+                    if (ow + s < a.Wo) {
+                        _Float16 v = epilogue(out[r][s], a.bias, k, relu0);
+                        if (res)
+                            v = add_residual(
+                                v,
+                                __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
+                                                                 rrs, row + 2 * s, 0, 0)),
+                                a.relu);
+                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
+                                                              row + 2 * s, 0, 0);
+                    }
             }
         }
     }
@@ -337,6 +352,7 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     BlockArgs a;
     a.bias = reinterpret_cast<const _Float16*>(ep.bias);
     a.relu = ep.relu;
+    a.residual = reinterpret_cast<const _Float16*>(ep.residual);
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
     a.xd = (int)(xp & 15);
@@ -364,7 +380,11 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.cp = p.cp;
     a.nj = p.nj;
     a.chan2 = (2 * H * W) & 15;
-    a.y_pairs = (Wo % 2 == 0 && (reinterpret_cast<uintptr_t>(y) & 3) == 0) ? 1 : 0;
+    a.y_pairs = (Wo % 2 == 0 &&
+                 ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(ep.residual)) & 3) ==
+                     0)
+                    ? 1
+                    : 0;
     fused_block_kernel<<<dim3((unsigned)p.grid), dim3(kBT), 0, s>>>(a);
     return hipGetLastError();
 }

@@ -24,6 +24,7 @@ void set_error(int code, const char* fmt, ...);
 struct Epilogue {
     const uint16_t* bias = nullptr;
     int relu = 0;
+    const uint16_t* residual = nullptr;  // fp16, the output's layout (added after the bias)
 };
 
 // Minimal tiling used by the product path: ceil(Ho/6) x ceil(Wo/6) tiles.
@@ -37,8 +38,8 @@ inline int pad8(int c) { return (c + 7) & ~7; }
 hipError_t launch_filter_transform_ref(const float* w, uint16_t* U, int K, int C,
                                        hipStream_t s);
 // Product layout: U[p][k][Cp], zero for c >= C (Cp = pad8(C)).
-hipError_t launch_filter_transform_gemm(const float* w, uint16_t* U, int K, int C, int Cp,
-                                        hipStream_t s);
+hipError_t launch_filter_transform_gemm(const void* w, bool w_f16, uint16_t* U, int K, int C,
+                                        int Cp, hipStream_t s);
 
 // Fragment-ordered copy of U for the fused kernels: for each position p, 16-row
 // output-channel tile kt and 16-channel step ks, the v_mfma_f32_16x16x16_f16 A

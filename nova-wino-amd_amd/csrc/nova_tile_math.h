@@ -37,6 +37,27 @@ __device__ __forceinline__ _Float16 epilogue(float v, const _Float16* bias, int 
     return h;
 }
 
+// Residual stage of the epilogue, after the bias: h plus the residual value
+// r (fp16 + fp16 summed in fp32, rounded once -- a separate `y + residual` on
+// fp16 tensors), then the optional ReLU. With a residual the ReLU is applied
+// here and not in epilogue().
+__device__ __forceinline__ _Float16 add_residual(_Float16 h, _Float16 r, int relu) {
+    _Float16 o = to_f16((float)h + (float)r);
+    if (relu && (float)o < 0.0f) o = (_Float16)0.0f;
+    return o;
+}
+
+// add_residual on two packed halves (low half = lower address).
+__device__ __forceinline__ unsigned add_residual2(unsigned h2, unsigned r2, int relu) {
+    const _Float16 lo = add_residual(__builtin_bit_cast(_Float16, (unsigned short)(h2 & 0xffffu)),
+                                     __builtin_bit_cast(_Float16, (unsigned short)(r2 & 0xffffu)),
+                                     relu);
+    const _Float16 hi = add_residual(__builtin_bit_cast(_Float16, (unsigned short)(h2 >> 16)),
+                                     __builtin_bit_cast(_Float16, (unsigned short)(r2 >> 16)), relu);
+    return (unsigned)__builtin_bit_cast(unsigned short, lo) |
+           ((unsigned)__builtin_bit_cast(unsigned short, hi) << 16);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
 // L2. This bijection maps the dispatch index L (0..N-1) to a work index such
 // that every XCD receives one contiguous range of work items, so spatial

@@ -22,8 +22,8 @@ namespace nova {
 // ---------------------------------------------------------------------------
 // Filter transform: one thread per (k, c) pair computes all 64 positions.
 // ---------------------------------------------------------------------------
-template <bool kRefLayout>
-__global__ __launch_bounds__(256) void filter_transform_kernel(const float* __restrict__ w,
+template <bool kRefLayout, typename WT>
+__global__ __launch_bounds__(256) void filter_transform_kernel(const WT* __restrict__ w,
                                                                _Float16* __restrict__ U, int K,
                                                                int C, int Cp) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -41,9 +41,10 @@ __global__ __launch_bounds__(256) void filter_transform_kernel(const float* __re
     float u[8][8];
     if (c < C) {
         float f[3][3];
-        const float* wp = w + ((int64_t)k * C + c) * 9;
+        // fp16 weights widen to fp32 exactly: the same U as their fp32 copy
+        const WT* wp = w + ((int64_t)k * C + c) * 9;
 #pragma unroll
-        for (int i = 0; i < 9; i++) f[i / 3][i % 3] = wp[i];
+        for (int i = 0; i < 9; i++) f[i / 3][i % 3] = (float)wp[i];
         filter_tile(f, u);
     } else {
 #pragma unroll
@@ -68,17 +69,21 @@ hipError_t launch_filter_transform_ref(const float* w, uint16_t* U, int K, int C
                                        hipStream_t s) {
     const int64_t n = (int64_t)K * C;
     const int64_t blocks = (n + 255) / 256;
-    filter_transform_kernel<true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+    filter_transform_kernel<true, float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
         w, reinterpret_cast<_Float16*>(U), K, C, C);
     return hipGetLastError();
 }
 
-hipError_t launch_filter_transform_gemm(const float* w, uint16_t* U, int K, int C, int Cp,
-                                        hipStream_t s) {
+hipError_t launch_filter_transform_gemm(const void* w, bool w_f16, uint16_t* U, int K, int C,
+                                        int Cp, hipStream_t s) {
     const int64_t n = (int64_t)K * Cp;
     const int64_t blocks = (n + 255) / 256;
-    filter_transform_kernel<false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
-        w, reinterpret_cast<_Float16*>(U), K, C, Cp);
+    if (w_f16)
+        filter_transform_kernel<false, _Float16><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+            static_cast<const _Float16*>(w), reinterpret_cast<_Float16*>(U), K, C, Cp);
+    else
+        filter_transform_kernel<false, float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+            static_cast<const float*>(w), reinterpret_cast<_Float16*>(U), K, C, Cp);
     return hipGetLastError();
 }
 
@@ -463,7 +468,7 @@ template <int TW, int kVW>
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
-    const _Float16* __restrict__ bias, int relu) {
+    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
     using G = OutGeom<TW>;
     __shared__ __align__(16) _Float16 sy[G::kKB * G::kPlane];
     const int nwb = (nw + TW - 1) / TW;
@@ -495,7 +500,8 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
 #pragma unroll
         for (int r = 0; r < 6; r++)
 #pragma unroll
-            for (int s = 0; s < 6; s++) sp[r * G::kCols + s] = epilogue(out[r][s], bias, kb, relu);
+            for (int s = 0; s < 6; s++)
+                sp[r * G::kCols + s] = epilogue(out[r][s], bias, kb, res ? 0 : relu);
     }
     __syncthreads();
 
@@ -516,25 +522,47 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     int sg = rem - r * nseg;
     const int dk = 256 / per_k, drem = 256 - dk * per_k;
     const int dr = drem / nseg, ds = drem - dr * nseg;
+    // residual (same layout as y): added per stored segment, then the ReLU
+    const __amdgpu_buffer_rsrc_t rrs = make_rsrc(res, res ? y_bytes : 0);
     for (; e < total; e += 256) {
         const _Float16* src = sy + kk * G::kPlane + r * G::kCols + sg * kVW;
         const int off = ybase + 2 * ((kk * Ho + r) * Wo + sg * kVW);
         if (sg * kVW + kVW <= ncols) {
             if constexpr (kVW == 4) {
                 typedef unsigned u2 __attribute__((ext_vector_type(2)));
-                __builtin_amdgcn_raw_buffer_store_b64(*reinterpret_cast<const u2*>(src), yrs, off,
-                                                      0, 0);
+                u2 v = *reinterpret_cast<const u2*>(src);
+                if (res) {
+                    const u2 rv = __builtin_bit_cast(
+                        u2, __builtin_amdgcn_raw_buffer_load_b64(rrs, off, 0, 0));
+                    v = u2{add_residual2(v[0], rv[0], relu), add_residual2(v[1], rv[1], relu)};
+                }
+                __builtin_amdgcn_raw_buffer_store_b64(v, yrs, off, 0, 0);
             } else if constexpr (kVW == 2) {
-                __builtin_amdgcn_raw_buffer_store_b32(*reinterpret_cast<const unsigned*>(src),
-                                                      yrs, off, 0, 0);
+                unsigned v = *reinterpret_cast<const unsigned*>(src);
+                if (res) v = add_residual2(v, __builtin_amdgcn_raw_buffer_load_b32(rrs, off, 0, 0),
+                                           relu);
+                __builtin_amdgcn_raw_buffer_store_b32(v, yrs, off, 0, 0);
             } else {
-                __builtin_amdgcn_raw_buffer_store_b16(*reinterpret_cast<const uint16_t*>(src),
-                                                      yrs, off, 0, 0);
+                _Float16 v = *src;
+                if (res)
+                    v = add_residual(v, __builtin_bit_cast(_Float16,
+                                                           __builtin_amdgcn_raw_buffer_load_b16(
+                                                               rrs, off, 0, 0)),
+                                     relu);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs, off,
+                                                      0, 0);
             }
         } else {
-            for (int q = 0; sg * kVW + q < ncols; q++)
-                __builtin_amdgcn_raw_buffer_store_b16(
-                    *reinterpret_cast<const uint16_t*>(src + q), yrs, off + 2 * q, 0, 0);
+            for (int q = 0; sg * kVW + q < ncols; q++) {
+                _Float16 v = src[q];
+                if (res)
+                    v = add_residual(v, __builtin_bit_cast(_Float16,
+                                                           __builtin_amdgcn_raw_buffer_load_b16(
+                                                               rrs, off + 2 * q, 0, 0)),
+                                     relu);
+                __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
+                                                      off + 2 * q, 0, 0);
+            }
         }
         sg += ds;
         r += dr;
@@ -554,17 +582,17 @@ template <int TW>
 static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, _Float16* yh,
                           int K, int Ho, int Wo, int nh, int nw, int ldm, int64_t pstride,
                           int kblocks, int64_t m_bytes, int64_t y_bytes, const _Float16* bias,
-                          int relu) {
+                          int relu, const _Float16* res) {
     const dim3 block(256);
     if (vw == 4)
         output_transform_kernel<TW, 4><<<grid, block, 0, s>>>(
-            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu);
+            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
     else if (vw == 2)
         output_transform_kernel<TW, 2><<<grid, block, 0, s>>>(
-            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu);
+            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
     else
         output_transform_kernel<TW, 1><<<grid, block, 0, s>>>(
-            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu);
+            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
 }
 
 // ---------------------------------------------------------------------------
@@ -581,7 +609,7 @@ static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, 
 __global__ __launch_bounds__(256) void output_lp_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int nkg, int64_t m_bytes, int64_t y_bytes, int pairs,
-    const _Float16* __restrict__ bias, int relu) {
+    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
     __shared__ float tls[4 * 8 * kLpPitch];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -624,24 +652,37 @@ __global__ __launch_bounds__(256) void output_lp_kernel(
 #pragma unroll
             for (int q = 0; q < 8; q++)
                 if (kAh[s2][q] != 0.0f) acc = __builtin_fmaf(t[q], kAh[s2][q], acc);
-            out[s2] = epilogue(acc, bias, k, relu);
+            out[s2] = epilogue(acc, bias, k, res ? 0 : relu);
         }
         const int ow = 6 * tw;
         const int row = 2 * (((b * K + k) * Ho + oh) * Wo + ow);
+        const __amdgpu_buffer_rsrc_t rrs = make_rsrc(res, res ? y_bytes : 0);
         if (pairs) {
 #pragma unroll
             for (int s2 = 0; s2 < 6; s2 += 2)
-                if (ow + s2 < Wo)
-                    __builtin_amdgcn_raw_buffer_store_b32(
-                        (unsigned)__builtin_bit_cast(uint16_t, out[s2]) |
-                            ((unsigned)__builtin_bit_cast(uint16_t, out[s2 + 1]) << 16),
-                        yrs, row + 2 * s2, 0, 0);
+                if (ow + s2 < Wo) {
+                    unsigned v = (unsigned)__builtin_bit_cast(uint16_t, out[s2]) |
+                                 ((unsigned)__builtin_bit_cast(uint16_t, out[s2 + 1]) << 16);
+                    if (res)
+                        v = add_residual2(
+                            v, __builtin_amdgcn_raw_buffer_load_b32(rrs, row + 2 * s2, 0, 0),
+                            relu);
+                    __builtin_amdgcn_raw_buffer_store_b32(v, yrs, row + 2 * s2, 0, 0);
+                }
         } else {
 #pragma unroll
             for (int s2 = 0; s2 < 6; s2++)
-                if (ow + s2 < Wo)
-                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, out[s2]),
-                                                          yrs, row + 2 * s2, 0, 0);
+                if (ow + s2 < Wo) {
+                    _Float16 v = out[s2];
+                    if (res)
+                        v = add_residual(v,
+                                         __builtin_bit_cast(_Float16,
+                                                            __builtin_amdgcn_raw_buffer_load_b16(
+                                                                rrs, row + 2 * s2, 0, 0)),
+                                         relu);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
+                                                          row + 2 * s2, 0, 0);
+                }
         }
     }
 }
@@ -656,11 +697,16 @@ static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K,
     if (y_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     // 4-byte pairs: every pair starts at an even column of a row whose pitch
     // is even, in a 4-byte aligned y
-    const int pairs = (Wo % 2 == 0 && (reinterpret_cast<uintptr_t>(y) & 3) == 0) ? 1 : 0;
+    const int pairs = (Wo % 2 == 0 &&
+                       ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(ep.residual)) &
+                        3) == 0)
+                          ? 1
+                          : 0;
     output_lp_kernel<<<dim3((unsigned)items), dim3(256), 0, s>>>(
         reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
         ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
-        reinterpret_cast<const _Float16*>(ep.bias), ep.relu);
+        reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
+        reinterpret_cast<const _Float16*>(ep.residual));
     return hipGetLastError();
 }
 
@@ -679,7 +725,9 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
     if (y_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     // widest row segment: every segment start must be aligned to its width
     // (tw0*6 columns is a multiple of 12, so the row pitch decides)
-    const uintptr_t ya = reinterpret_cast<uintptr_t>(y);
+    // (a residual is read with the same widths, so it must share the alignment)
+    const _Float16* res = reinterpret_cast<const _Float16*>(ep.residual);
+    const uintptr_t ya = reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(ep.residual);
     const int vw = (Wo % 4 == 0 && ya % 8 == 0) ? 4 : (Wo % 2 == 0 && ya % 4 == 0) ? 2 : 1;
     const dim3 grid((unsigned)nblocks);
     const _Float16* Mh = reinterpret_cast<const _Float16*>(M);
@@ -688,15 +736,15 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
     switch (tw) {
         case 2:
             launch_out_tw<2>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
-                             m_bytes, y_bytes, bias, ep.relu);
+                             m_bytes, y_bytes, bias, ep.relu, res);
             break;
         case 4:
             launch_out_tw<4>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
-                             m_bytes, y_bytes, bias, ep.relu);
+                             m_bytes, y_bytes, bias, ep.relu, res);
             break;
         default:
             launch_out_tw<8>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
-                             m_bytes, y_bytes, bias, ep.relu);
+                             m_bytes, y_bytes, bias, ep.relu, res);
             break;
     }
     return hipGetLastError();

@@ -57,7 +57,7 @@ class _Handle:
     """Owns one library handle; destroyed with the Python object (at
     interpreter exit the process releases device memory itself)."""
 
-    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "w_ref")
+    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "w_ref", "res_ptr")
 
     def __init__(self):
         self.lib = get_lib()
@@ -68,6 +68,7 @@ class _Handle:
         self.bias_key = None
         self.bias16 = None
         self.w_ref = None
+        self.res_ptr = None
 
     def set_weights_cached(self, weight):
         """Transform the filter unless this exact tensor object, unchanged
@@ -99,6 +100,13 @@ class _Handle:
             check("set_epilogue")
             self.bias_key = key
 
+    def set_residual(self, residual):
+        """Residual operand of the next launch (None: none)."""
+        p = residual.data_ptr() if residual is not None else None
+        if p != self.res_ptr:
+            self.lib.nova_set_residual(self.h, p)
+            self.res_ptr = p
+
     def set_stream(self, device):
         s = current_stream_ptr(device)
         if s != self.stream:
@@ -106,12 +114,18 @@ class _Handle:
             self.stream = s
 
     def set_weights(self, weight):
-        # fp32 contiguous copy at the boundary: the library reads fp32
-        # [K,C,3,3]; the conversion also makes a .half()'d module safe. The
-        # temporary stays valid for the asynchronous transform because both
-        # run on the current stream (the caching allocator is stream-ordered).
-        w32 = weight.detach().to(torch.float32).contiguous()
-        self.lib.nova_set_weights(self.h, ptr(w32), w32.shape[0], w32.shape[1])
+        # fp16 weights (a .half()'d module) go to the library as they are,
+        # anything else as an fp32 contiguous copy; both give the same
+        # transform. A temporary stays valid for the asynchronous transform
+        # because both run on the current stream (the caching allocator is
+        # stream-ordered).
+        w = weight.detach()
+        if w.dtype == torch.float16:
+            w = w.contiguous()
+            self.lib.nova_set_weights_f16(self.h, ptr(w), w.shape[0], w.shape[1])
+        else:
+            w = w.to(torch.float32).contiguous()
+            self.lib.nova_set_weights(self.h, ptr(w), w.shape[0], w.shape[1])
         check("set_weights")
 
     def __del__(self):
@@ -367,7 +381,7 @@ class NovaWinogradConv2d(nn.Module):
         return self._tiling
 
     # -- forward ------------------------------------------------------------
-    def _run(self, x, bias):
+    def _run(self, x, bias, residual=None):
         """Launch the HIP path on a contiguous fp16 input; returns fp16."""
         require_gpu_tensor(x, "input")
         B, C, H, W = x.shape
@@ -377,6 +391,13 @@ class NovaWinogradConv2d(nn.Module):
         nh, nw, H_out, W_out = self._ensure_workspace(B, H, W)
         hd = self._handle
         hd.set_bias(bias)
+        if residual is not None:
+            require_gpu_tensor(residual, "residual")
+            if (residual.dtype != torch.float16 or not residual.is_contiguous()
+                    or tuple(residual.shape) != (B, self.out_channels, H_out, W_out)):
+                raise ValueError("residual must be a contiguous float16 tensor of the "
+                                 f"output's shape {(B, self.out_channels, H_out, W_out)}")
+        hd.set_residual(residual)
         output = torch.empty(B, self.out_channels, H_out, W_out, dtype=torch.float16,
                              device=x.device)
         V, M = self._V_gemm, self._M_gemm
@@ -389,12 +410,15 @@ class NovaWinogradConv2d(nn.Module):
         check("forward")
         return output
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """y = conv(x) (+ bias). ``residual`` (an extension): a float16
+        tensor of the output's shape added after the bias, with the rounding
+        of a separate ``y + residual``."""
         # Fast path: the same input shape, weight and bias objects at the same
         # versions, and the same current stream as the previous call -- only
         # the output allocation and the launch remain.
         st = self._state
-        if st is not None:
+        if st is not None and residual is None:
             w, b = self.weight, self.bias
             if (x.shape == st[0] and w is st[1] and w._version == st[2]
                     and w.data_ptr() == st[13] and b is st[3]
@@ -410,8 +434,11 @@ class NovaWinogradConv2d(nn.Module):
         assert x.dtype == torch.float16, f"Input must be float16, got {x.dtype}"
         assert x.is_contiguous(), "Input must be contiguous"
         assert x.dim() == 4 and x.shape[1] == self.in_channels
-        out = self._run(x, self.bias)
-        self._remember(x)
+        out = self._run(x, self.bias, residual)
+        if residual is None:
+            self._remember(x)
+        else:
+            self._state = None  # the next call clears the residual on the full path
         return out
 
     def _remember(self, x):

@@ -54,6 +54,8 @@ _SIGNATURES = {
     "nova_set_stream": (None, [_vp, _vp]),
     "nova_set_path": (None, [_vp, _i]),
     "nova_set_epilogue": (None, [_vp, _vp, _i]),
+    "nova_set_weights_f16": (None, [_vp, _vp, _i, _i]),
+    "nova_set_residual": (None, [_vp, _vp]),
     "nova_get_last_path": (_i, [_vp]),
     "nova_workspace_bytes": (ctypes.c_longlong, [_vp, _i, _i, _i, _i]),
     "nova_profile_enable": (None, [_vp, _i]),
@@ -154,19 +156,24 @@ def compute_tiling(H, W, pad):
     return nh.value, nw.value, H_out.value, W_out.value
 
 
-def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False):
+def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False, residual=None):
     """Functional API: NOVA Winograd F(6,3) forward pass
     (/root/reference/nova_winograd/ops.py:147-176).
 
     Args:
         input_fp16:  [B, C, H, W] float16 tensor on GPU.
-        weight_fp32: [K, C, 3, 3] float32 tensor on GPU.
+        weight_fp32: [K, C, 3, 3] float32 tensor on GPU (float16 is accepted
+                     too, as an extension, and gives the same result as its
+                     float32 copy).
         padding:     Convolution padding (default 1).
         bias:        optional [K] tensor on GPU, added in the output transform
                      with the rounding of ``output + bias.half()`` (an
                      extension: the reference has no bias here).
         relu:        clamp negative outputs to zero in the same pass
                      (extension).
+        residual:    optional float16 tensor of the output's shape, added
+                     after the bias and before the ReLU with the rounding of a
+                     separate ``output + residual`` (extension).
 
     Returns:
         output: [B, K, H_out, W_out] float16 tensor on GPU.
@@ -179,7 +186,7 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False):
     require_gpu_tensor(input_fp16, "input")
     require_gpu_tensor(weight_fp32, "weight")
     assert input_fp16.dtype == torch.float16
-    assert weight_fp32.dtype == torch.float32
+    assert weight_fp32.dtype in (torch.float32, torch.float16)
     assert input_fp16.is_contiguous() and weight_fp32.is_contiguous()
     assert input_fp16.dim() == 4 and weight_fp32.dim() == 4
     assert tuple(weight_fp32.shape[1:]) == (input_fp16.shape[1], 3, 3)
@@ -189,6 +196,10 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False):
     nh, nw, H_out, W_out = compute_tiling(H, W, padding)
     output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=input_fp16.device)
 
+    if residual is not None:
+        require_gpu_tensor(residual, "residual")
+        assert residual.dtype == torch.float16 and residual.is_contiguous()
+        assert tuple(residual.shape) == (B, K, H_out, W_out)
     bias16 = None
     if bias is not None:
         require_gpu_tensor(bias, "bias")
@@ -197,12 +208,17 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False):
     handle = _lib.nova_create()
     try:
         _lib.nova_set_stream(handle, current_stream_ptr(input_fp16.device))
-        _lib.nova_set_weights(handle, ptr(weight_fp32), K, C)
+        if weight_fp32.dtype == torch.float16:
+            _lib.nova_set_weights_f16(handle, ptr(weight_fp32), K, C)
+        else:
+            _lib.nova_set_weights(handle, ptr(weight_fp32), K, C)
         check("set_weights")
         if bias16 is not None or relu:
             _lib.nova_set_epilogue(handle, ptr(bias16) if bias16 is not None else None,
                                    1 if relu else 0)
             check("set_epilogue")
+        if residual is not None:
+            _lib.nova_set_residual(handle, ptr(residual))
         _lib.nova_forward(handle, ptr(input_fp16), ptr(output), B, H, W, padding)
         check("forward")
     finally:
