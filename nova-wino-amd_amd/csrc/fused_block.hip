@@ -98,6 +98,7 @@ __device__ __forceinline__ void load_u(const BlockArgs& a, const __amdgpu_buffer
     }
 }
 
+template <int NJ>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     __shared__ __align__(16) unsigned char lds[kBLdsBytes];
     unsigned char* xs = lds;
@@ -131,25 +132,28 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     const int tl = t0 + (tile_ok ? t : 0);
     const int th = tl / a.nw, tw = tl - (tl / a.nw) * a.nw;
     const int rb0 = 6 * (th - th_first) * a.rp + 12 * tw;
-    unsigned rr0 = 0, rmask = 0, cmask = 0;
+    unsigned rr0 = 0, cmask = 0;
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) {
         const int h = 6 * th - a.pad + ii;
-        rmask |= (tile_ok && h >= 0 && h < a.H) ? (1u << ii) : 0u;
         rr0 |= (unsigned)((a.xd + 2 * (b * a.C * HW + h * a.W - a.pad)) & 15) << (4 * ii);
         const int w = 6 * tw - a.pad + ii;
         cmask |= (w >= 0 && w < a.W) ? (1u << ii) : 0u;
     }
+    // column mask as four dword masks over the packed halves
+    unsigned dm[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        dm[q] = (((cmask >> (2 * q)) & 1u) ? 0xffffu : 0u) |
+                (((cmask >> (2 * q + 1)) & 1u) ? 0xffff0000u : 0u);
 
-    // ---- staging pieces: e = (channel c, staged row rs, 16-byte column j) ----
-    const int per_c = rows_st * a.nj;
-    const int total = kBCC * per_c;
-    const int e_c = tid / per_c;
-    const int e_rem = tid - e_c * per_c;
-    const int e_r = e_rem / a.nj;
-    const int e_j = e_rem - e_r * a.nj;
-    const int dc = kBT / per_c, drem = kBT - dc * per_c;
-    const int dr = drem / a.nj, dj = drem - dr * a.nj;
+    // ---- staging spans: (channel c, staged row r), kSpr per thread per round ----
+    // Each span is NJ 16-byte loads at immediate offsets, all of a round in
+    // flight at once (two spans per round while their registers fit beside
+    // the accumulators, else one); rows outside the image and channels past C
+    // get an out-of-range offset, so zeros are staged for them.
+    constexpr int kSpr = NJ <= 5 ? 2 : 1;
+    const int nspans = kBCC * rows_st;
 
     f4 acc[8][4];
 #pragma unroll
@@ -159,43 +163,36 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 
     for (int c0 = 0; c0 < a.Cp; c0 += kBCC) {
         __syncthreads();  // the previous chunk is done with the staging area and V
-        // -- stage the chunk's input rows: four loads in flight per round --
-        {
-            int c = e_c, r = e_r, j = e_j;
-            for (int e = tid; e < total; e += 4 * kBT) {
-                u4 v[4];
-                int dst[4];
+        // -- stage the chunk's input rows --
+        for (int sp0 = 0; sp0 < nspans; sp0 += kSpr * kBT) {
+            u4 v[kSpr][NJ];
+            int dst[kSpr];
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const int h = h_first + r;
-                    const int cg = c0 + c;
-                    const bool ok = e + u * kBT < total && h >= 0 && h < a.H && cg < a.C;
-                    const int o = a.xd + 2 * ((b * a.C + cg) * HW + h * a.W - a.pad);
-                    v[u] = ok ? __builtin_amdgcn_raw_buffer_load_b128(xrs, (o & ~15) + 16 * j, 0, 0)
-                              : u4{0u, 0u, 0u, 0u};
-                    dst[u] = ok ? c * a.cp + r * a.rp + 16 * j : -1;
-                    j += dj;
-                    r += dr;
-                    c += dc;
-                    if (j >= a.nj) {
-                        j -= a.nj;
-                        r++;
-                    }
-                    if (r >= rows_st) {
-                        r -= rows_st;
-                        c++;
-                    }
-                }
+            for (int u = 0; u < kSpr; u++) {
+                const int sp = sp0 + tid + u * kBT;
+                const int c = sp / rows_st, r = sp - (sp / rows_st) * rows_st;
+                const int h = h_first + r;
+                const int cg = c0 + c;
+                const bool live = sp < nspans;
+                const int o = a.xd + 2 * ((b * a.C + cg) * HW + h * a.W - a.pad);
+                const int base = (live && h >= 0 && h < a.H && cg < a.C) ? (o & ~15) : kBOob;
+                dst[u] = live ? c * a.cp + r * a.rp : -1;
 #pragma unroll
-                for (int u = 0; u < 4; u++)
-                    if (dst[u] >= 0) *reinterpret_cast<u4*>(xs + dst[u]) = v[u];
+                for (int q = 0; q < NJ; q++)
+                    v[u][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + 16 * q, 0, 0);
             }
+#pragma unroll
+            for (int u = 0; u < kSpr; u++)
+                if (dst[u] >= 0) {
+#pragma unroll
+                    for (int q = 0; q < NJ; q++)
+                        *reinterpret_cast<u4*>(xs + dst[u] + 16 * q) = v[u][q];
+                }
         }
         __syncthreads();
         // -- input transform of (channel c0 + ct, tile t) into V --
         {
             const int cg = c0 + ct;
-            const unsigned rm = cg < a.C ? rmask : 0u;
             const unsigned char* cbase = xs + ct * a.cp + rb0;
             unsigned d4[8][4];
 #pragma unroll
@@ -210,14 +207,20 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 for (int q = 0; q < 4; q++)
                     d4[ii][q] = __builtin_amdgcn_alignbyte(w5[q + 1], w5[q], (unsigned)(rho & 3));
             }
+            // edge tiles: zero the columns outside the image (rows outside it
+            // and channels past C were staged as zeros)
+            if (cmask != 0xffu) {
+#pragma unroll
+                for (int ii = 0; ii < 8; ii++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) d4[ii][q] &= dm[q];
+            }
             input_tile_rows(
                 [&](int ii, int j) {
                     const unsigned pr = d4[ii][j >> 1];
                     const unsigned short bits =
                         (unsigned short)((j & 1) ? (pr >> 16) : (pr & 0xffffu));
-                    return ((rm >> ii) & (cmask >> j) & 1u)
-                               ? (float)__builtin_bit_cast(_Float16, bits)
-                               : 0.0f;
+                    return (float)__builtin_bit_cast(_Float16, bits);
                 },
                 [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
         }
@@ -334,7 +337,7 @@ bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
     const int rows_st = 6 * maxrows + 2;
     const int rp = round16i(2 * (6 * nw + 2) + 18);
     const int cp = rows_st * rp + 16;
-    if (kBCC * cp > kBXBytes) return false;
+    if (kBCC * cp > kBXBytes || rp / 16 > 10) return false;
     p->nruns = nruns;
     p->n_kblk = (K + 63) / 64;
     p->rp = rp;
@@ -385,7 +388,19 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
                      0)
                     ? 1
                     : 0;
-    fused_block_kernel<<<dim3((unsigned)p.grid), dim3(kBT), 0, s>>>(a);
+    const dim3 grid((unsigned)p.grid), block(kBT);
+    switch (p.nj) {
+        case 2: fused_block_kernel<2><<<grid, block, 0, s>>>(a); break;
+        case 3: fused_block_kernel<3><<<grid, block, 0, s>>>(a); break;
+        case 4: fused_block_kernel<4><<<grid, block, 0, s>>>(a); break;
+        case 5: fused_block_kernel<5><<<grid, block, 0, s>>>(a); break;
+        case 6: fused_block_kernel<6><<<grid, block, 0, s>>>(a); break;
+        case 7: fused_block_kernel<7><<<grid, block, 0, s>>>(a); break;
+        case 8: fused_block_kernel<8><<<grid, block, 0, s>>>(a); break;
+        case 9: fused_block_kernel<9><<<grid, block, 0, s>>>(a); break;
+        case 10: fused_block_kernel<10><<<grid, block, 0, s>>>(a); break;
+        default: return hipErrorInvalidConfiguration;
+    }
     return hipGetLastError();
 }
 
