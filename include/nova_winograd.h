@@ -130,6 +130,12 @@ NOVA_API void nova_set_path(nova_handle_t h, int path);
  * separate elementwise op after the convolution
  * (/root/reference/nova_winograd/conv2d.py:240-241). */
 NOVA_API void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu);
+/* Activation layout of every subsequent forward on the handle: 0 = NCHW
+ * (default, the reference's), 1 = NHWC (channels last): x is [B][H][W][C]
+ * and y (and a residual) [B][Ho][Wo][K]. NHWC runs the three-pass pipeline
+ * with channels-last transform kernels; results equal the NCHW path's, bit
+ * for bit, in the other layout. No counterpart in the reference. */
+NOVA_API void nova_set_layout(nova_handle_t h, int nhwc);
 /* Residual of every subsequent forward on the handle: an fp16 tensor with the
  * output's shape and layout [B][K][Ho][Wo], added after the bias and before
  * the ReLU (each add rounded to fp16, as separate `y + bias.half()` and

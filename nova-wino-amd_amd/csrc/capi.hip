@@ -79,6 +79,7 @@ struct Handle {
     hipStream_t stream = nullptr;
     int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block
     Epilogue ep;        // bias / ReLU applied by every forward
+    int nhwc = 0;       // 1: x and y are NHWC (channels last)
     int last_path = 0;
     bool ready = false;
     Profiler prof;
@@ -214,7 +215,7 @@ bool fused_block_plan_for(const Handle* Hd, const Shape& s, FusedBlockPlan* p) {
 // (tile block). A requested fused variant outside its envelope falls back to
 // the three-pass pipeline.
 int choose_path(const Handle* Hd, const Shape& s) {
-    if (Hd->path_pref == 1) return 1;
+    if (Hd->path_pref == 1 || Hd->nhwc) return 1;  // the fused kernels read and write NCHW
     if (Hd->path_pref == 2) {
         FusedPlan p;
         return fused_plan_for(Hd, s, &p) ? 2 : 1;
@@ -240,14 +241,15 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
     const hipStream_t st = Hd->stream;
     const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
     const uint16_t* U = Hd->U;
+    const bool nhwc = Hd->nhwc != 0;
     auto in = [=]() {
         return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp,
-                                      (int64_t)Cp * s.BP, st);
+                                      (int64_t)Cp * s.BP, st, nhwc);
     };
     auto gm = [=]() { return launch_wgemm(U, V, M, K, Cp, (int)s.BP, st); };
     auto out = [=]() {
         return launch_output_transform(M, y, s.B, K, s.Ho, s.Wo, s.nh, s.nw, K,
-                                       (int64_t)K * s.BP, st, ep);
+                                       (int64_t)K * s.BP, st, ep, nhwc);
     };
     if (remember) {
         pf.last[kKindInput] = in;
@@ -614,6 +616,16 @@ void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu) {
     }
     H->ep.bias = static_cast<const uint16_t*>(d_bias_f16);
     H->ep.relu = relu;
+}
+
+void nova_set_layout(nova_handle_t h, int nhwc) {
+    Handle* H = as_handle(h, "nova_set_layout");
+    if (!H) return;
+    if (nhwc != 0 && nhwc != 1) {
+        set_error(kErrInvalidArgument, "nova_set_layout: nhwc must be 0 or 1");
+        return;
+    }
+    H->nhwc = nhwc;
 }
 
 void nova_set_residual(nova_handle_t h, const void* d_residual_f16) {

@@ -54,16 +54,17 @@ hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStre
 
 // ---- input transform -----------------------------------------------------
 // V[p*pstride + bp*ldv + c], bp = (b*nh + th)*nw + tw, for th < nh, tw < nw.
-// Channels c in [C, ldv) are written as zero.
+// Channels c in [C, ldv) are written as zero. x is NCHW, or NHWC if nhwc.
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s);
+                                  hipStream_t s, bool nhwc = false);
 
 // ---- output transform ----------------------------------------------------
-// Reads M[p*pstride + bp*ldm + k]; writes y[b][k][h][w] for h < Ho, w < Wo.
+// Reads M[p*pstride + bp*ldm + k]; writes y[b][k][h][w] (y[b][h][w][k] if
+// nhwc) for h < Ho, w < Wo.
 hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K, int Ho,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
-                                   hipStream_t s, Epilogue ep = Epilogue());
+                                   hipStream_t s, Epilogue ep = Epilogue(), bool nhwc = false);
 
 // ---- Winograd-domain batched GEMM ------------------------------------------
 // For p in 0..63: M_p[bp][k] = sum_c U_p[k][c] * V_p[bp][c]  (fp32 accumulate,

@@ -283,6 +283,74 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Input transform, NHWC (channels-last) x, tile-block form. Workgroup = one
+// tile row x TW tiles x 256/TW channels, as for NCHW. Staging: the strip's 8
+// rows x (6*TW + 2) pixels x the block's channels, 16-byte loads of 8
+// channels of one pixel (pixels outside the image and channels past C read
+// zero through out-of-range offsets), into LDS as [row][pixel][channel] with
+// the channel run padded by 8 halves. Compute: thread (channel cc, tile t)
+// reads its 64 values as 2-byte LDS reads (lanes over consecutive channels,
+// consecutive addresses), the shared FMA chains, and stores V like the NCHW
+// kernel. Zero padding is already in LDS, so no masks. Needs C % 8 == 0 and a
+// 16-byte aligned x (the launcher checks; otherwise the lane-parallel form).
+// ---------------------------------------------------------------------------
+template <int TW>
+__global__ __launch_bounds__(256) void input_nhwc_kernel(
+    const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
+    int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int64_t v_bytes) {
+    constexpr int kCB = 256 / TW;
+    constexpr int kCols = 6 * TW + 2;
+    constexpr int kPix = kCB + 8;            // halves per staged pixel
+    constexpr int kGroups = kCB / 8;         // 16-byte channel groups per pixel
+    constexpr int kUnits = 8 * kCols * kGroups;
+    constexpr int kRounds = (kUnits + 255) / 256;
+    __shared__ __align__(16) _Float16 sx[8 * kCols * kPix];
+    const int nwb = (nw + TW - 1) / TW;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int tw0 = (L % nwb) * TW;
+    const int th = (L / nwb) % nh;
+    const int bz = L / (nwb * nh);
+    const int b = bz / cblocks;
+    const int c0 = (bz % cblocks) * kCB;
+    const int h0 = th * 6 - pad, w0 = tw0 * 6 - pad;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, x_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
+    {
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        u4 val[kRounds];
+        int dst[kRounds];
+#pragma unroll
+        for (int u = 0; u < kRounds; u++) {
+            const int e = threadIdx.x + 256 * u;
+            const int g = e % kGroups, pix = (e / kGroups) % kCols, r = e / (kGroups * kCols);
+            const int h = h0 + r, w = w0 + pix, c = c0 + 8 * g;
+            const bool ok = e < kUnits && h >= 0 && h < H && w >= 0 && w < W && c < C;
+            val[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                xrs, ok ? 2 * (((b * H + h) * W + w) * C + c) : kOob, 0, 0);
+            dst[u] = e < kUnits ? (r * kCols + pix) * kPix + 8 * g : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kRounds; u++)
+            if (dst[u] >= 0) *reinterpret_cast<u4*>(sx + dst[u]) = val[u];
+    }
+    __syncthreads();
+    const int cc = threadIdx.x % kCB;
+    const int t = threadIdx.x / kCB;
+    const int tw = tw0 + t;
+    const int c = c0 + cc;
+    const int bp = (b * nh + th) * nw + tw;
+    const int voff = (tw < nw && c < ldv) ? 2 * (bp * ldv + c) : kOob;
+    const _Float16* src = sx + 6 * t * kPix + cc;
+    input_tile_rows([&](int i, int j) { return (float)src[(i * kCols + j) * kPix]; },
+                    [&](int r, int s2, float v) {
+                        const int p = r * 8 + s2;
+                        __builtin_amdgcn_raw_buffer_store_b16(
+                            __builtin_bit_cast(uint16_t, to_f16(v)), vrs, voff,
+                            (int)(2 * p * pstride), 0);
+                    });
+}
+
+// ---------------------------------------------------------------------------
 // Input transform, lane-parallel form: 8 lanes per (tile, channel) patch, so a
 // wave carries 8 channels of one tile and a thread's instruction chain is an
 // eighth of the one-patch-per-thread form (short latency at batch 1, many
@@ -299,6 +367,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kLpPitch = 72;  // floats per channel in the transpose buffer
 
+template <bool kNhwc>
 __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restrict__ x,
                                                        _Float16* __restrict__ V, int C, int H,
                                                        int W, int pad, int nh, int nw, int ldv,
@@ -319,12 +388,15 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
 
     const bool ok = c < C && w >= 0 && w < W;
-    const int base = 2 * ((b * C + (ok ? c : 0)) * H * W + w);
+    // element (b, c, h, w): NCHW ((b*C + c)*H + h)*W + w, NHWC ((b*H + h)*W + w)*C + c
+    const int cc = ok ? c : 0, ww = ok ? w : 0;
+    const int base = kNhwc ? 2 * ((b * H * W + ww) * C + cc) : 2 * ((b * C + cc) * H * W + ww);
+    const int rstep = kNhwc ? 2 * W * C : 2 * W;
     float d[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int h = h0 + i;
-        const int off = (ok && h >= 0 && h < H) ? base + 2 * h * W : kOob;
+        const int off = (ok && h >= 0 && h < H) ? base + h * rstep : kOob;
         d[i] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
                                                        xrs, off, 0, 0));
     }
@@ -355,15 +427,20 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
 
 static hipError_t launch_input_lp(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s) {
+                                  hipStream_t s, bool nhwc) {
     const int ncg = (ldv + 31) / 32;
     const int64_t items = (int64_t)B * nh * nw * ncg;
     if (items >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
     const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
-    input_lp_kernel<<<dim3((unsigned)items), dim3(256), 0, s>>>(
-        reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad, nh,
-        nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
+    if (nhwc)
+        input_lp_kernel<true><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+            reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
+            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
+    else
+        input_lp_kernel<false><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+            reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
+            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
     return hipGetLastError();
 }
 
@@ -408,10 +485,32 @@ static bool latency_bound(int64_t rows, int n, int ch) {
 
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s) {
-    if (latency_bound((int64_t)B * nh, nw, ldv))
-        return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s);
+                                  hipStream_t s, bool nhwc) {
+    if (latency_bound((int64_t)B * nh, nw, ldv) ||
+        (nhwc && (C % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0)))
+        return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, nhwc);
     const int tw = pick_tw((int64_t)B * nh, nw, ldv);
+    if (nhwc) {
+        const int cb = 256 / tw;
+        const int cblocks = (ldv + cb - 1) / cb;
+        const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * cblocks;
+        const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
+        if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
+        if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
+        const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+        _Float16* Vh = reinterpret_cast<_Float16*>(V);
+        const dim3 grid((unsigned)nblocks), block(256);
+        if (tw == 2)
+            input_nhwc_kernel<2><<<grid, block, 0, s>>>(xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
+                                                        cblocks, (int)x_bytes, 2 * 64 * pstride);
+        else if (tw == 4)
+            input_nhwc_kernel<4><<<grid, block, 0, s>>>(xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
+                                                        cblocks, (int)x_bytes, 2 * 64 * pstride);
+        else
+            input_nhwc_kernel<8><<<grid, block, 0, s>>>(xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
+                                                        cblocks, (int)x_bytes, 2 * 64 * pstride);
+        return hipGetLastError();
+    }
     const int cb = 256 / tw;
     const int cblocks = (ldv + cb - 1) / cb;
     const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * cblocks;
@@ -578,6 +677,62 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Output transform, NHWC (channels-last) y, tile-block form: thread (tile, k)
+// reads its 64 positions as in the NCHW kernel and stores its 36 outputs
+// straight to y[b][h][w][k] -- lanes over consecutive k, so every store
+// instruction writes 128 contiguous bytes and no LDS transpose is needed.
+// The epilogue (bias, residual in y's layout, ReLU) is applied per value.
+// ---------------------------------------------------------------------------
+template <int TW>
+__global__ __launch_bounds__(256) void output_nhwc_kernel(
+    const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
+    int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
+    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
+    constexpr int kKB = 256 / TW;
+    const int nwb = (nw + TW - 1) / TW;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int tw0 = (L % nwb) * TW;
+    const int th = (L / nwb) % nh;
+    const int bz = L / (nwb * nh);
+    const int b = bz / kblocks;
+    const int k0 = (bz % kblocks) * kKB;
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, m_bytes);
+    const __amdgpu_buffer_rsrc_t yrs = make_rsrc(y, y_bytes);
+    const __amdgpu_buffer_rsrc_t rrs = make_rsrc(res, res ? y_bytes : 0);
+    const int kk = threadIdx.x % kKB;
+    const int t = threadIdx.x / kKB;
+    const int tw = tw0 + t;
+    const int k = k0 + kk;
+    if (tw >= nw || k >= K) return;
+    const int bp = (b * nh + th) * nw + tw;
+    const int moff = 2 * (bp * ldm + k);
+    uint16_t m[64];
+#pragma unroll
+    for (int p = 0; p < 64; p++)
+        m[p] = __builtin_amdgcn_raw_buffer_load_b16(mrs, moff, (int)(2 * p * pstride), 0);
+    float out[6][6];
+    output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
+                out);
+    const int oh = 6 * th, ow = 6 * tw;
+#pragma unroll
+    for (int r = 0; r < 6; r++) {
+        if (oh + r >= Ho) break;
+#pragma unroll
+        for (int s2 = 0; s2 < 6; s2++) {
+            if (ow + s2 >= Wo) break;
+            const int off = 2 * (((b * Ho + oh + r) * Wo + ow + s2) * K + k);
+            _Float16 v = epilogue(out[r][s2], bias, k, res ? 0 : relu);
+            if (res)
+                v = add_residual(
+                    v,
+                    __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(rrs, off, 0, 0)),
+                    relu);
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs, off, 0, 0);
+        }
+    }
+}
+
 template <int TW>
 static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, _Float16* yh,
                           int K, int Ho, int Wo, int nh, int nw, int ldm, int64_t pstride,
@@ -606,6 +761,7 @@ static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, 
 // else six halves; rows past Ho and columns past Wo are skipped).
 // Workgroup = 4 waves = 32 output channels of one tile.
 // ---------------------------------------------------------------------------
+template <bool kNhwc>
 __global__ __launch_bounds__(256) void output_lp_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int nkg, int64_t m_bytes, int64_t y_bytes, int pairs,
@@ -655,8 +811,27 @@ __global__ __launch_bounds__(256) void output_lp_kernel(
             out[s2] = epilogue(acc, bias, k, res ? 0 : relu);
         }
         const int ow = 6 * tw;
-        const int row = 2 * (((b * K + k) * Ho + oh) * Wo + ow);
         const __amdgpu_buffer_rsrc_t rrs = make_rsrc(res, res ? y_bytes : 0);
+        if (kNhwc) {
+            // y[b][oh][ow + s][k]: lanes over channels, one half per pixel
+            const int pix = 2 * (((b * Ho + oh) * Wo + ow) * K + k);
+#pragma unroll
+            for (int s2 = 0; s2 < 6; s2++)
+                if (ow + s2 < Wo) {
+                    const int off = pix + 2 * s2 * K;
+                    _Float16 v = out[s2];
+                    if (res)
+                        v = add_residual(v,
+                                         __builtin_bit_cast(_Float16,
+                                                            __builtin_amdgcn_raw_buffer_load_b16(
+                                                                rrs, off, 0, 0)),
+                                         relu);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs, off,
+                                                          0, 0);
+                }
+            return;
+        }
+        const int row = 2 * (((b * K + k) * Ho + oh) * Wo + ow);
         if (pairs) {
 #pragma unroll
             for (int s2 = 0; s2 < 6; s2 += 2)
@@ -689,7 +864,7 @@ __global__ __launch_bounds__(256) void output_lp_kernel(
 
 static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K, int Ho, int Wo,
                                    int nh, int nw, int ldm, int64_t pstride, hipStream_t s,
-                                   Epilogue ep) {
+                                   Epilogue ep, bool nhwc) {
     const int nkg = (K + 31) / 32;
     const int64_t items = (int64_t)B * nh * nw * nkg;
     if (items >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
@@ -702,19 +877,53 @@ static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K,
                         3) == 0)
                           ? 1
                           : 0;
-    output_lp_kernel<<<dim3((unsigned)items), dim3(256), 0, s>>>(
-        reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
-        ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
-        reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
-        reinterpret_cast<const _Float16*>(ep.residual));
+    if (nhwc)
+        output_lp_kernel<true><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+            reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
+            ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
+            reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
+            reinterpret_cast<const _Float16*>(ep.residual));
+    else
+        output_lp_kernel<false><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+            reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
+            ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
+            reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
+            reinterpret_cast<const _Float16*>(ep.residual));
     return hipGetLastError();
 }
 
 hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K, int Ho,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
-                                   hipStream_t s, Epilogue ep) {
+                                   hipStream_t s, Epilogue ep, bool nhwc) {
     if (latency_bound((int64_t)B * nh, nw, K))
-        return launch_output_lp(M, y, B, K, Ho, Wo, nh, nw, ldm, pstride, s, ep);
+        return launch_output_lp(M, y, B, K, Ho, Wo, nh, nw, ldm, pstride, s, ep, nhwc);
+    if (nhwc) {
+        const int tw = pick_tw((int64_t)B * nh, nw, K);
+        const int kb = 256 / tw;
+        const int kblocks = (K + kb - 1) / kb;
+        const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * kblocks;
+        const int64_t y_bytes = 2 * (int64_t)B * K * Ho * Wo;
+        if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
+        if (y_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
+        const _Float16* Mh = reinterpret_cast<const _Float16*>(M);
+        _Float16* yh = reinterpret_cast<_Float16*>(y);
+        const _Float16* bias = reinterpret_cast<const _Float16*>(ep.bias);
+        const _Float16* res = reinterpret_cast<const _Float16*>(ep.residual);
+        const dim3 grid((unsigned)nblocks), block(256);
+        if (tw == 2)
+            output_nhwc_kernel<2><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+                                                         kblocks, 2 * 64 * pstride, y_bytes, bias,
+                                                         ep.relu, res);
+        else if (tw == 4)
+            output_nhwc_kernel<4><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+                                                         kblocks, 2 * 64 * pstride, y_bytes, bias,
+                                                         ep.relu, res);
+        else
+            output_nhwc_kernel<8><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+                                                         kblocks, 2 * 64 * pstride, y_bytes, bias,
+                                                         ep.relu, res);
+        return hipGetLastError();
+    }
     const _Float16* bias = reinterpret_cast<const _Float16*>(ep.bias);
     const int tw = pick_tw((int64_t)B * nh, nw, K);
     const int kb = 256 / tw;

@@ -42,6 +42,13 @@ def _weight_key(weight):
             tuple(weight.shape), weight.device)
 
 
+def _is_nhwc(x):
+    """True for a channels-last 4-d tensor that is not also NCHW-contiguous
+    (those run the NHWC kernels)."""
+    return (x.dim() == 4 and not x.is_contiguous()
+            and x.is_contiguous(memory_format=torch.channels_last))
+
+
 _exiting = False
 
 
@@ -57,7 +64,7 @@ class _Handle:
     """Owns one library handle; destroyed with the Python object (at
     interpreter exit the process releases device memory itself)."""
 
-    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "w_ref", "res_ptr")
+    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "w_ref", "res_ptr", "nhwc")
 
     def __init__(self):
         self.lib = get_lib()
@@ -69,6 +76,7 @@ class _Handle:
         self.bias16 = None
         self.w_ref = None
         self.res_ptr = None
+        self.nhwc = 0
 
     def set_weights_cached(self, weight):
         """Transform the filter unless this exact tensor object, unchanged
@@ -99,6 +107,13 @@ class _Handle:
             self.lib.nova_set_epilogue(self.h, ptr(self.bias16), 0)
             check("set_epilogue")
             self.bias_key = key
+
+    def set_layout(self, nhwc):
+        """Activation layout of the next launches: 0 NCHW, 1 NHWC."""
+        if nhwc != self.nhwc:
+            self.lib.nova_set_layout(self.h, nhwc)
+            check("set_layout")
+            self.nhwc = nhwc
 
     def set_residual(self, residual):
         """Residual operand of the next launch (None: none)."""
@@ -382,24 +397,29 @@ class NovaWinogradConv2d(nn.Module):
 
     # -- forward ------------------------------------------------------------
     def _run(self, x, bias, residual=None):
-        """Launch the HIP path on a contiguous fp16 input; returns fp16."""
+        """Launch the HIP path on a contiguous (NCHW) or channels-last (NHWC)
+        fp16 input; returns fp16 in the same memory format."""
         require_gpu_tensor(x, "input")
         B, C, H, W = x.shape
+        nhwc = _is_nhwc(x)
         if C != self.in_channels:
             raise ValueError(f"expected {self.in_channels} input channels, got {C}")
         self._ensure_handle()
         nh, nw, H_out, W_out = self._ensure_workspace(B, H, W)
         hd = self._handle
         hd.set_bias(bias)
+        fmt = torch.channels_last if nhwc else torch.contiguous_format
         if residual is not None:
             require_gpu_tensor(residual, "residual")
-            if (residual.dtype != torch.float16 or not residual.is_contiguous()
+            if (residual.dtype != torch.float16 or not residual.is_contiguous(memory_format=fmt)
                     or tuple(residual.shape) != (B, self.out_channels, H_out, W_out)):
-                raise ValueError("residual must be a contiguous float16 tensor of the "
-                                 f"output's shape {(B, self.out_channels, H_out, W_out)}")
+                raise ValueError("residual must be a float16 tensor of the output's shape "
+                                 f"{(B, self.out_channels, H_out, W_out)} in the input's "
+                                 "memory format")
+        hd.set_layout(1 if nhwc else 0)
         hd.set_residual(residual)
         output = torch.empty(B, self.out_channels, H_out, W_out, dtype=torch.float16,
-                             device=x.device)
+                             device=x.device, memory_format=fmt)
         V, M = self._V_gemm, self._M_gemm
         hd.lib.nova_forward_workspace(
             hd.h, x.data_ptr(), output.data_ptr(),
@@ -432,13 +452,15 @@ class NovaWinogradConv2d(nn.Module):
                     check("forward")
                 return out
         assert x.dtype == torch.float16, f"Input must be float16, got {x.dtype}"
-        assert x.is_contiguous(), "Input must be contiguous"
+        assert x.is_contiguous() or _is_nhwc(x), \
+            "Input must be contiguous (NCHW) or channels_last"
         assert x.dim() == 4 and x.shape[1] == self.in_channels
         out = self._run(x, self.bias, residual)
-        if residual is None:
+        if residual is None and x.is_contiguous():
             self._remember(x)
         else:
-            self._state = None  # the next call clears the residual on the full path
+            # the next call resets the residual / layout on the full path
+            self._state = None
         return out
 
     def _remember(self, x):

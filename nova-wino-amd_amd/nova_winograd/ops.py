@@ -56,6 +56,7 @@ _SIGNATURES = {
     "nova_set_epilogue": (None, [_vp, _vp, _i]),
     "nova_set_weights_f16": (None, [_vp, _vp, _i, _i]),
     "nova_set_residual": (None, [_vp, _vp]),
+    "nova_set_layout": (None, [_vp, _i]),
     "nova_get_last_path": (_i, [_vp]),
     "nova_workspace_bytes": (ctypes.c_longlong, [_vp, _i, _i, _i, _i]),
     "nova_profile_enable": (None, [_vp, _i]),
@@ -187,18 +188,22 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False, resi
     require_gpu_tensor(weight_fp32, "weight")
     assert input_fp16.dtype == torch.float16
     assert weight_fp32.dtype in (torch.float32, torch.float16)
-    assert input_fp16.is_contiguous() and weight_fp32.is_contiguous()
+    nhwc = (input_fp16.dim() == 4 and not input_fp16.is_contiguous()
+            and input_fp16.is_contiguous(memory_format=torch.channels_last))
+    assert (input_fp16.is_contiguous() or nhwc) and weight_fp32.is_contiguous()
     assert input_fp16.dim() == 4 and weight_fp32.dim() == 4
     assert tuple(weight_fp32.shape[1:]) == (input_fp16.shape[1], 3, 3)
 
     B, C, H, W = input_fp16.shape
     K = weight_fp32.shape[0]
     nh, nw, H_out, W_out = compute_tiling(H, W, padding)
-    output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=input_fp16.device)
+    fmt = torch.channels_last if nhwc else torch.contiguous_format
+    output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=input_fp16.device,
+                         memory_format=fmt)
 
     if residual is not None:
         require_gpu_tensor(residual, "residual")
-        assert residual.dtype == torch.float16 and residual.is_contiguous()
+        assert residual.dtype == torch.float16 and residual.is_contiguous(memory_format=fmt)
         assert tuple(residual.shape) == (B, K, H_out, W_out)
     bias16 = None
     if bias is not None:
@@ -219,6 +224,8 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False, resi
             check("set_epilogue")
         if residual is not None:
             _lib.nova_set_residual(handle, ptr(residual))
+        if nhwc:
+            _lib.nova_set_layout(handle, 1)
         _lib.nova_forward(handle, ptr(input_fp16), ptr(output), B, H, W, padding)
         check("forward")
     finally:

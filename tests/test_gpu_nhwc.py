@@ -1,0 +1,109 @@
+"""Channels-last (NHWC) activations (nova_set_layout; no counterpart in the
+reference): for every shape class -- lane-parallel transforms (small
+problems), tile-block NHWC transforms (large ones), C not a multiple of 8 and
+an x that is not 16-byte aligned (lane-parallel fallback), odd output widths,
+pad 0 and 2 -- the NHWC forward must equal the NCHW three-pass forward bit for
+bit, in the other memory format; likewise with the bias/residual/ReLU
+epilogue, through the module (channels_last in, channels_last out) and the
+functional API. The NCHW path is itself parity-tested against the oracle.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+CL = torch.channels_last
+
+
+def _run(x, w, pad, nhwc, bias=None, relu=0, res=None, path=0):
+    from nova_winograd.ops import check, get_lib
+
+    lib = get_lib()
+    B, C, H, W = x.shape
+    K = w.shape[0]
+    Ho, Wo = H + 2 * pad - 2, W + 2 * pad - 2
+    y = torch.empty(B, K, Ho, Wo, dtype=torch.float16, device=DEV,
+                    memory_format=CL if nhwc else torch.contiguous_format)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_path(h, path)
+        lib.nova_set_layout(h, 1 if nhwc else 0)
+        lib.nova_set_weights(h, w.data_ptr(), K, C)
+        lib.nova_set_epilogue(h, bias.data_ptr() if bias is not None else None, relu)
+        lib.nova_set_residual(h, res.data_ptr() if res is not None else None)
+        lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, W, pad)
+        check()
+        took = lib.nova_get_last_path(h)
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    return y, took
+
+
+CASES = [
+    (1, 64, 64, 56, 1),     # lane-parallel both ways
+    (8, 64, 64, 56, 1),     # tile-block NHWC kernels
+    (32, 128, 128, 28, 1),
+    (4, 256, 200, 14, 1),
+    (12, 40, 24, 30, 1),
+    (3, 20, 36, 17, 2),     # C % 8 != 0: lane-parallel input
+    (16, 24, 16, 13, 0),    # odd output width, pad 0
+]
+
+
+@pytest.mark.parametrize("B,C,K,H,pad", CASES)
+def test_nhwc_equals_nchw(B, C, K, H, pad):
+    print(f"[nhwc] B={B} C={C} K={K} H={H} pad={pad}", flush=True)
+    torch.manual_seed(12)
+    x = torch.randn(B, C, H, H, device=DEV).half()
+    w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
+    y_ref, took_ref = _run(x, w, pad, False, path=1)
+    y, took = _run(x.contiguous(memory_format=CL), w, pad, True)
+    assert took == 1
+    assert y.is_contiguous(memory_format=CL)
+    assert torch.equal(y, y_ref)
+    # epilogue in NHWC: bias, residual (channels-last), ReLU
+    bias = (torch.randn(K, device=DEV) * 0.5).half()
+    res = torch.randn_like(y_ref).contiguous(memory_format=CL)
+    y_e, _ = _run(x.contiguous(memory_format=CL), w, pad, True, bias=bias, relu=1, res=res)
+    yb_ref, _ = _run(x, w, pad, False, bias=bias, path=1)
+    assert torch.equal(y_e, torch.relu(yb_ref + res))
+
+
+def test_nhwc_unaligned_input():
+    torch.manual_seed(13)
+    B, C, K, H = 8, 64, 64, 56
+    x = torch.randn(B, C, H, H, device=DEV).half()
+    w = (torch.randn(K, C, 3, 3, device=DEV) * 0.06).float()
+    y_ref, _ = _run(x, w, 1, False, path=1)
+    n = x.numel()
+    store = torch.empty(n + 8, dtype=torch.float16, device=DEV)
+    x_cl = torch.as_strided(store, (B, C, H, H), (H * H * C, 1, H * C, C), storage_offset=1)
+    x_cl.copy_(x)
+    assert x_cl.is_contiguous(memory_format=CL) and x_cl.data_ptr() % 16 != 0
+    y, _ = _run(x_cl, w, 1, True)
+    assert torch.equal(y, y_ref)
+
+
+def test_module_and_functional_channels_last():
+    from nova_winograd import NovaWinogradConv2d, nova_forward
+
+    torch.manual_seed(14)
+    conv = NovaWinogradConv2d(64, 48, kernel_size=3, padding=1, bias=True).to(DEV)
+    with torch.no_grad():
+        conv.bias.copy_(torch.randn(48))
+    x = torch.randn(4, 64, 28, 28, device=DEV).half()
+    xc = x.contiguous(memory_format=CL)
+    with torch.no_grad():
+        y = conv(x)
+        yc = conv(xc)
+        y2 = conv(x)  # back to NCHW: the layout is reset
+        y3 = conv(x)  # cached path
+        yf = nova_forward(xc, conv.weight, padding=1, bias=conv.bias)
+    torch.cuda.synchronize()
+    assert yc.is_contiguous(memory_format=CL) and not yc.is_contiguous()
+    assert torch.equal(yc, y)
+    assert torch.equal(y2, y) and torch.equal(y3, y)
+    assert yf.is_contiguous(memory_format=CL) and torch.equal(yf, y)
