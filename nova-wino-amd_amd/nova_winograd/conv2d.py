@@ -13,6 +13,7 @@ fallback (a CPU input raises).
 """
 
 import atexit
+import ctypes
 import math
 import threading
 import weakref
@@ -40,6 +41,28 @@ def _weight_key(weight):
     alone, /root/reference/nova_winograd/conv2d.py:195-203.)"""
     return (id(weight), weight._version, weight.data_ptr(), weight.dtype,
             tuple(weight.shape), weight.device)
+
+
+_FASTCALL = []  # [forward_ws or None], resolved once
+
+
+def _fastcall(lib):
+    """The CPython fast-call binding of nova_forward_workspace (one foreign
+    call that also raises on a library error), or None when it is not built;
+    the cached forward path then uses ctypes."""
+    if not _FASTCALL:
+        fn = None
+        try:
+            from nova_winograd import _nova_call
+
+            addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value  # noqa: E731
+            _nova_call.bind(addr(lib.nova_forward_workspace), addr(lib.nova_get_last_error),
+                            addr(lib.nova_get_last_error_message))
+            fn = _nova_call.forward_ws
+        except ImportError:
+            pass
+        _FASTCALL.append(fn)
+    return _FASTCALL[0]
 
 
 def _is_nhwc(x):
@@ -448,7 +471,7 @@ class NovaWinogradConv2d(nn.Module):
                     and _raw_stream(st[6]) == st[7]):
                 out = torch.empty(st[8], dtype=torch.float16, device=st[5])
                 st[9](st[10], x.data_ptr(), out.data_ptr(), *st[11])
-                if st[12]():
+                if st[12] is not None and st[12]():
                     check("forward")
                 return out
         assert x.dtype == torch.float16, f"Input must be float16, got {x.dtype}"
@@ -473,14 +496,16 @@ class NovaWinogradConv2d(nn.Module):
         V, M = self._V_gemm, self._M_gemm
         w, b = self.weight, self.bias
         idx = x.device.index if x.device.index is not None else torch.cuda.current_device()
+        fast = _fastcall(hd.lib)
         self._state = (
             x.shape, w, w._version, b, None if b is None else (b._version, b.data_ptr()),
             x.device, idx,
-            hd.stream, (B, self.out_channels, H_out, W_out), hd.lib.nova_forward_workspace,
+            hd.stream, (B, self.out_channels, H_out, W_out),
+            fast if fast is not None else hd.lib.nova_forward_workspace,
             hd.h,
             (V.data_ptr() if V is not None else None, M.data_ptr() if M is not None else None,
              B, H, W, self.padding, nh, nw),
-            hd.lib.nova_get_last_error,
+            None if fast is not None else hd.lib.nova_get_last_error,
             w.data_ptr(),
         )
 

@@ -92,3 +92,28 @@ def test_entry_points_reject_bad_shapes_without_gpu(lib):
     assert lib.nova_get_last_error() == 1
     lib.nova_filter_transform(None, None, 4, 4)
     assert lib.nova_get_last_error() == 1
+
+
+def test_fastcall_binding_raises_library_errors(lib):
+    """The CPython fast-call binding of nova_forward_workspace (the module's
+    cached path) reports library errors as RuntimeError; exercised on a handle
+    without weights, which the library refuses before any GPU work."""
+    import ctypes
+
+    from nova_winograd import _nova_call
+    from nova_winograd.conv2d import _fastcall
+
+    fwd = _fastcall(lib)
+    assert fwd is _nova_call.forward_ws
+    h = lib.nova_create()
+    try:
+        with pytest.raises(RuntimeError, match="weights"):
+            fwd(h, 1, 2, None, None, 1, 8, 8, 1, 2, 2)
+        assert lib.nova_get_last_error() == 0  # the binding consumed the error
+        with pytest.raises(TypeError):
+            fwd(h, 1, 2)
+    finally:
+        lib.nova_destroy(h)
+    with pytest.raises(ValueError):
+        _nova_call.bind(0, 0, 0)
+    assert ctypes.cast(lib.nova_forward_workspace, ctypes.c_void_p).value
