@@ -143,6 +143,13 @@ def pmc_workload(runs, reps, torch):
     torch.cuda.synchronize()
 
 
+# Kernel families: the library reports one name per pipeline stage; the
+# lane-parallel and channels-last forms belong to the stage's family.
+KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_kernel",
+                                            "input_nhwc_kernel"),
+                 "output_transform_kernel": ("output_transform_kernel", "output_lp_kernel",
+                                             "output_nhwc_kernel")}
+
 NOVA_KERNELS = ["input_transform_kernel", "output_transform_kernel",
                 "wgemm_kernel<1, 1, 4, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2>",
                 "wgemm_lds_kernel<128, 128, 2, 2>", "fused_block_kernel", "fused_kernel<1>",
@@ -154,6 +161,8 @@ def _name_keys(name):
     Itanium-mangled (int template arguments only), for matching rocprofv3
     records; trailing template arguments the library's short name leaves
     out (tuning depths) still match."""
+    if name in KERNEL_FAMILY:
+        return list(KERNEL_FAMILY[name])
     if "<" not in name:
         return [name]
     base, args = name.split("<", 1)
@@ -220,7 +229,47 @@ def traffic_from(fetch_dir, write_dir, out_path):
                 "fetch_kib_by_grid": fetch[name][1], "write_kib_by_grid": write[name][1]})
     with open(out_path, "w") as f:
         json.dump(data, f, indent=1)
+    write_traffic_summary(data, os.path.join(os.path.dirname(out_path),
+                                             "traffic_resnet50_3x3s1_b1_b32.md"))
     print(json.dumps(data))
+
+
+def write_traffic_summary(data, path):
+    """Markdown summary of traffic.json (the figures the bench line uses)."""
+    lines = [
+        "# HBM traffic per launch, library kernels, ResNet-50 3x3 s1 layers at B=1 and B=32",
+        "",
+        "Commands (from the repository root, on one MI355X; two passes, one counter each):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp && cd -",
+        "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o pmc -- "
+        "python3 -u bench.py --pmc-mode",
+        "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc -- "
+        "python3 -u bench.py --pmc-mode",
+        "python3 bench.py --traffic-from gpurun_out/pmc_fetch gpurun_out/pmc_write   "
+        "# -> profiles/traffic.json + this file",
+        "```",
+        "",
+        f"Calibration: the same run launches one elementwise kernel that reads and writes "
+        f"{COPY_MIB} MiB. FETCH_SIZE read {data['fetch_copy_kib']} KiB for its "
+        f"{COPY_MIB * 1024} KiB of reads (scale {data['fetch_scale']}), WRITE_SIZE "
+        f"{data['write_copy_kib']} KiB for its writes (scale {data['write_scale']}). Every "
+        "kernel's counters are multiplied by these factors.",
+        "",
+        "| kernel | grid (threads) | FETCH KiB (raw) | WRITE KiB | HBM MB (scaled) |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for k in data["kernels"]:
+        writes = dict(k["write_kib_by_grid"])
+        for grid, fkib in k["fetch_kib_by_grid"]:
+            wkib = writes.get(grid, 0.0)
+            mb = (fkib * data["fetch_scale"] + wkib * data["write_scale"]) * 1024 / 1e6
+            lines.append(f"| `{k['kernel']}` | {grid} | {fkib} | {wkib} | {mb:.3f} |")
+        lines.append(f"| **{k['kernel']} mean per launch** | | | | "
+                     f"**{k['hbm_bytes_per_launch'] / 1e6:.3f}** |")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
 
 
 def cpu_baseline(layers_spec, budget_s, threads):
@@ -353,9 +402,20 @@ def extra_measurements(runs, lib, torch, nn, nw, reps):
             nova(x)
             t16 = time_region(lambda: m16(x), 20, torch)
             tn = time_region(lambda: nova(x), 20, torch)
-        out["resnet50"].append({"B": B, "miopen_ms": round(t16, 4), "nova_ms": round(tn, 4),
-                                "speedup": round(t16 / tn, 3)})
-        log(f"resnet50 B={B:<3d} model forward: miopen {t16:8.3f} ms  nova {tn:8.3f} ms")
+            # the eager forward is bound by Python launch overhead (~160 modules);
+            # HIP-graph replay shows the GPU time of each model
+            g16, gn = graph_of(lambda: m16(x), torch), graph_of(lambda: nova(x), torch)
+            tg16 = time_region(g16.replay, 20, torch) if g16 is not None else None
+            tgn = time_region(gn.replay, 20, torch) if gn is not None else None
+        rec = {"B": B, "miopen_ms": round(t16, 4), "nova_ms": round(tn, 4),
+               "speedup": round(t16 / tn, 3)}
+        if tg16 is not None and tgn is not None:
+            rec.update({"miopen_graph_ms": round(tg16, 4), "nova_graph_ms": round(tgn, 4),
+                        "graph_speedup": round(tg16 / tgn, 3)})
+        out["resnet50"].append(rec)
+        log(f"resnet50 B={B:<3d} model forward: miopen {t16:8.3f} ms  nova {tn:8.3f} ms"
+            + (f"  | graph: miopen {tg16:7.3f} ms  nova {tgn:7.3f} ms"
+               if tg16 is not None and tgn is not None else ""))
         del m16, nova, x
     # cold-cache times of the headline layers
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
