@@ -87,7 +87,8 @@ class _Handle:
     """Owns one library handle; destroyed with the Python object (at
     interpreter exit the process releases device memory itself)."""
 
-    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "w_ref", "res_ptr", "nhwc")
+    __slots__ = ("h", "lib", "stream", "key", "bias_key", "bias16", "b_ref", "w_ref", "res_ptr",
+                 "nhwc")
 
     def __init__(self):
         self.lib = get_lib()
@@ -95,8 +96,9 @@ class _Handle:
         check("create")
         self.stream = 0
         self.key = None
-        self.bias_key = None
+        self.bias_key = (None, 0)  # the library's default epilogue: none
         self.bias16 = None
+        self.b_ref = None
         self.w_ref = None
         self.res_ptr = None
         self.nhwc = 0
@@ -113,23 +115,29 @@ class _Handle:
         self.set_weights(weight)
         self.w_ref = (weakref.ref(weight), key)
 
-    def set_bias(self, bias):
-        """Fuse the bias add into the output transform: the library adds an
-        fp16 copy of ``bias`` with the rounding of the reference's separate
-        ``output + bias.half()``. The copy is kept here while kernels may
-        read it and rebuilt when the parameter changes."""
+    def set_bias(self, bias, relu=0):
+        """Fuse the bias add (and optionally a ReLU) into the output
+        transform: the library adds an fp16 copy of ``bias`` with the rounding
+        of the reference's separate ``output + bias.half()``. The copy is kept
+        here while kernels may read it and rebuilt when the tensor (held by
+        weak reference), its version or its storage changes."""
         if bias is None:
-            if self.bias_key is not None:
-                self.lib.nova_set_epilogue(self.h, None, 0)
-                self.bias_key = None
+            if self.bias_key != (None, relu):
+                self.lib.nova_set_epilogue(self.h, None, relu)
+                check("set_epilogue")
+                self.bias_key = (None, relu)
                 self.bias16 = None
+                self.b_ref = None
             return
-        key = (id(bias), bias._version, bias.data_ptr(), bias.dtype)
-        if key != self.bias_key:
-            self.bias16 = bias.detach().to(torch.float16).contiguous()
-            self.lib.nova_set_epilogue(self.h, ptr(self.bias16), 0)
-            check("set_epilogue")
-            self.bias_key = key
+        key = (bias._version, bias.data_ptr(), bias.dtype, relu)
+        ref = self.b_ref
+        if ref is not None and ref() is bias and self.bias_key == key:
+            return
+        self.bias16 = bias.detach().to(torch.float16).contiguous()
+        self.lib.nova_set_epilogue(self.h, ptr(self.bias16), relu)
+        check("set_epilogue")
+        self.bias_key = key
+        self.b_ref = weakref.ref(bias)
 
     def set_layout(self, nhwc):
         """Activation layout of the next launches: 0 NCHW, 1 NHWC."""
@@ -259,6 +267,9 @@ def _register_custom_op():
             hd = _op_handle(x.device)
             hd.set_stream(x.device)
             hd.set_weights_cached(weight)
+            hd.set_bias(None)  # the handle is shared with nova_forward
+            hd.set_residual(None)
+            hd.set_layout(0)
             hd.lib.nova_forward(hd.h, ptr(x), ptr(output), B, H, W, padding)
             check("forward")
         return output

@@ -179,9 +179,11 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False, resi
     Returns:
         output: [B, K, H_out, W_out] float16 tensor on GPU.
 
-    Like the reference it creates a handle, transforms the filter, runs and
-    destroys the handle; all work is ordered on PyTorch's current stream, so
-    no device-wide synchronisation is needed around it.
+    Unlike the reference (a handle created, the filter transformed and the
+    device synchronised twice per call), it runs on one persistent handle per
+    device and transforms the filter only for a new weight tensor or a new
+    version of it; all work is ordered on PyTorch's current stream, so no
+    device-wide synchronisation is needed around it.
     """
     _ensure_lib()
     require_gpu_tensor(input_fp16, "input")
@@ -205,30 +207,25 @@ def nova_forward(input_fp16, weight_fp32, padding=1, bias=None, relu=False, resi
         require_gpu_tensor(residual, "residual")
         assert residual.dtype == torch.float16 and residual.is_contiguous(memory_format=fmt)
         assert tuple(residual.shape) == (B, K, H_out, W_out)
-    bias16 = None
     if bias is not None:
         require_gpu_tensor(bias, "bias")
         assert bias.numel() == K
-        bias16 = bias.detach().to(torch.float16).contiguous()
-    handle = _lib.nova_create()
-    try:
-        _lib.nova_set_stream(handle, current_stream_ptr(input_fp16.device))
-        if weight_fp32.dtype == torch.float16:
-            _lib.nova_set_weights_f16(handle, ptr(weight_fp32), K, C)
-        else:
-            _lib.nova_set_weights(handle, ptr(weight_fp32), K, C)
-        check("set_weights")
-        if bias16 is not None or relu:
-            _lib.nova_set_epilogue(handle, ptr(bias16) if bias16 is not None else None,
-                                   1 if relu else 0)
-            check("set_epilogue")
-        if residual is not None:
-            _lib.nova_set_residual(handle, ptr(residual))
-        if nhwc:
-            _lib.nova_set_layout(handle, 1)
-        _lib.nova_forward(handle, ptr(input_fp16), ptr(output), B, H, W, padding)
-        check("forward")
-    finally:
-        # nova_destroy frees device memory; hipFree waits for queued work.
-        _lib.nova_destroy(handle)
+    # One persistent handle per device, shared with the torch.compile op; the
+    # filter transform is cached for the exact weight tensor and version last
+    # used (the reference creates a handle, transforms the filter and
+    # synchronises twice per call, ops.py:166-174).
+    from nova_winograd.conv2d import _op_handle, _op_lock
+
+    with _op_lock:
+        hd = _op_handle(input_fp16.device)
+        hd.set_stream(input_fp16.device)
+        hd.set_weights_cached(weight_fp32)
+        hd.set_bias(bias, 1 if relu else 0)  # keeps an fp16 copy of bias
+        hd.set_residual(residual)
+        hd.set_layout(1 if nhwc else 0)
+        try:
+            _lib.nova_forward(hd.h, ptr(input_fp16), ptr(output), B, H, W, padding)
+            check("forward")
+        finally:
+            hd.set_residual(None)
     return output

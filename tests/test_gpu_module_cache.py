@@ -73,3 +73,37 @@ def test_cached_forward_invalidation():
         y7 = conv(x)  # back on the default stream
         assert torch.equal(y7, y4)
     torch.cuda.synchronize()
+
+
+def test_functional_cached_handle(monkeypatch):
+    """nova_forward runs on the persistent per-device handle: the filter is
+    transformed once for repeated calls with the same weight, again after an
+    in-place update, and a bias or residual of one call never leaks into the
+    next (temporaries included)."""
+    from nova_winograd import conv2d as cv
+    from nova_winograd import nova_forward
+
+    torch.manual_seed(15)
+    x = torch.randn(2, 16, 14, 14, device=DEV).half()
+    w = torch.randn(24, 16, 3, 3, device=DEV) * 0.1
+    calls = []
+    orig = cv._Handle.set_weights
+    monkeypatch.setattr(cv._Handle, "set_weights",
+                        lambda self, weight: (calls.append(1), orig(self, weight))[1])
+    y0 = nova_forward(x, w)
+    y1 = nova_forward(x, w)
+    assert torch.equal(y0, y1) and len(calls) == 1
+    yb = nova_forward(x, w, bias=torch.full((24,), 0.5, device=DEV))
+    yb2 = nova_forward(x, w, bias=torch.full((24,), -0.25, device=DEV))  # a new temporary
+    yr = nova_forward(x, w, residual=torch.ones_like(y0))
+    y2 = nova_forward(x, w)
+    torch.cuda.synchronize()
+    assert torch.equal(yb, y0 + torch.tensor(0.5, dtype=torch.float16, device=DEV))
+    assert torch.equal(yb2, y0 + torch.tensor(-0.25, dtype=torch.float16, device=DEV))
+    assert torch.equal(yr, y0 + 1)
+    assert torch.equal(y2, y0)  # neither bias nor residual left on the handle
+    with torch.no_grad():
+        w.mul_(2.0)
+    y3 = nova_forward(x, w)
+    assert len(calls) == 2
+    assert not torch.equal(y3, y0)
