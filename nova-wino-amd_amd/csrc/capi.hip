@@ -3,10 +3,11 @@
 // The handle replaces the reference's NovaWinogradF63 / NovaWinogradFused
 // host classes (/root/reference/csrc/nova_winograd.hip:456-611,
 // /root/reference/csrc/nova_winograd_fused.hip:446-607): it owns the
-// Winograd-domain filter U (product layout [64][K][Cp]) and a grow-only
-// workspace, launches on a caller-selected stream, and picks the fused or the
-// 3-pass pipeline per call. Errors are recorded per thread instead of exiting
-// the process.
+// Winograd-domain filter U (product layout [64][K][Cp], plus its MFMA
+// fragment-ordered copy for the fused kernels) and a grow-only workspace,
+// launches on a caller-selected stream in the caller-selected activation
+// layout, and picks the fused or the 3-pass pipeline per call. Errors are
+// recorded per thread instead of exiting the process.
 #include <cstdarg>
 #include <cstdio>
 #include <algorithm>
@@ -78,7 +79,7 @@ struct Handle {
     size_t cnt_cap = 0;       // counters
     hipStream_t stream = nullptr;
     int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block
-    Epilogue ep;        // bias / ReLU applied by every forward
+    Epilogue ep;        // bias / residual / ReLU applied by every forward
     int nhwc = 0;       // 1: x and y are NHWC (channels last)
     int last_path = 0;
     bool ready = false;
