@@ -133,8 +133,11 @@ NOVA_API void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int rel
 /* Activation layout of every subsequent forward on the handle: 0 = NCHW
  * (default, the reference's), 1 = NHWC (channels last): x is [B][H][W][C]
  * and y (and a residual) [B][Ho][Wo][K]. NHWC runs the three-pass pipeline
- * with channels-last transform kernels; results equal the NCHW path's, bit
- * for bit, in the other layout. No counterpart in the reference. */
+ * with channels-last transform kernels or, where it fits (C % 8 == 0 and a
+ * 16-byte aligned x), the tile-block fused kernel; the position-row fused
+ * kernel is NCHW only (path 2 runs 3-pass). Results equal the NCHW path's of
+ * the same kind, bit for bit, in the other layout. No counterpart in the
+ * reference. */
 NOVA_API void nova_set_layout(nova_handle_t h, int nhwc);
 /* Residual of every subsequent forward on the handle: an fp16 tensor with the
  * output's shape and layout [B][K][Ho][Wo], added after the bias and before

@@ -209,15 +209,17 @@ bool fused_block_plan_for(const Handle* Hd, const Shape& s, FusedBlockPlan* p) {
     if (!fused_fits(Bc * Hd->C * s.H * s.W, u_frag_elems(Hd->K, Hd->Cp),
                     Bc * Hd->K * s.Ho * s.Wo))
         return false;
-    return fused_block_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.nh, s.nw, p);
+    return fused_block_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.H, s.W, s.nh, s.nw, p,
+                            Hd->nhwc != 0);
 }
 
 // Pipeline for a forward: 1 three-pass, 2 fused (position-row split), 3 fused
 // (tile block). A requested fused variant outside its envelope falls back to
 // the three-pass pipeline.
 int choose_path(const Handle* Hd, const Shape& s) {
-    if (Hd->path_pref == 1 || Hd->nhwc) return 1;  // the fused kernels read and write NCHW
+    if (Hd->path_pref == 1) return 1;
     if (Hd->path_pref == 2) {
+        if (Hd->nhwc) return 1;  // the position-row kernel reads and writes NCHW only
         FusedPlan p;
         return fused_plan_for(Hd, s, &p) ? 2 : 1;
     }
@@ -227,10 +229,14 @@ int choose_path(const Handle* Hd, const Shape& s) {
     }
     // Automatic choice, from MI355X measurements: the tile-block fused kernel
     // wins for layers with at most 64 input and output channels once there
-    // are enough 16-tile runs to occupy the chip (ResNet-50 conv2_x at B=32:
-    // 32.6 us vs 41.3 us three-pass); everything else runs three-pass.
+    // are enough 16-tile runs to occupy the chip, and while each CU runs at
+    // most two of its workgroups one after the other (ResNet-50 conv2_x,
+    // NCHW: B=32 31.7 us vs 39.3 us three-pass, B=64 60.6 vs 65.4, but B=128
+    // 115 vs 112 and B=16 29.8 vs 25.4; NHWC: B=32 33.2 vs 36.2); everything
+    // else runs three-pass.
     FusedBlockPlan bp;
-    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp) && bp.grid >= 128)
+    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp) && bp.grid >= 128 &&
+        bp.grid <= 2 * 256)
         return 3;
     return 1;
 }
@@ -291,7 +297,9 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         set_error(kErrInvalidArgument, "%s: a single image of this shape exceeds 1 GB buffers", fn);
         return;
     }
-    const int path = choose_path(Hd, s_all);
+    int path = choose_path(Hd, s_all);
+    // the channels-last tile-block kernel stages x with 16-byte loads
+    if (path == 3 && Hd->nhwc && !aligned16(x)) path = 1;
     const bool fused = path != 1;
     if (path == 1 && Hd->path_pref >= 2) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
@@ -338,7 +346,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             const uint16_t* U = Hd->Uf;
             const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
             FusedBlockPlan bp;
-            if (!fused_block_plan((int)s.B, C, K, Cp, s.H, s.W, s.nh, s.nw, &bp)) {
+            if (!fused_block_plan((int)s.B, C, K, Cp, s.H, s.W, s.nh, s.nw, &bp,
+                                  Hd->nhwc != 0)) {
                 set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
                 return;
             }

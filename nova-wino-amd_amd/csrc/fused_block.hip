@@ -34,6 +34,7 @@ namespace nova {
 
 namespace {
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -66,6 +67,7 @@ struct BlockArgs {
     const _Float16* bias;  // output epilogue (null: none)
     int relu;
     const _Float16* residual;  // added after the bias, y's layout (null: none)
+    int cols;                  // NHWC: staged pixels per row (6*nw + 2)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -98,7 +100,19 @@ __device__ __forceinline__ void load_u(const BlockArgs& a, const __amdgpu_buffer
     }
 }
 
-template <int NJ>
+// kNhwc: x and y channels-last. The chunk is then staged as [row][pixel]
+// [channel] (kNhwcPix halves per pixel: 16-byte loads of 8 channels, zero for
+// pixels outside the image), the transform reads its patch with 2-byte LDS
+// reads, and the output phase runs with lanes over channels (128-byte NHWC
+// stores). NJ is unused (0) in that form.
+constexpr int kNhwcPix = 36;  // 72 bytes: tiles 6 pixels apart fall in distinct banks
+// NHWC keeps M as [tile][kk][position] (tile pitch padded by 16 bytes): the
+// output phase then reads consecutive channels per lane at a 144-byte stride,
+// and the MFMA write, with lanes over tiles, at a 16-byte offset per tile.
+constexpr int kNhwcTileP = 64 * 72 + 8;
+static_assert(16 * kNhwcTileP * 2 <= 160 * 1024, "NHWC M fits in LDS");
+
+template <int NJ, bool kNhwc>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     __shared__ __align__(16) unsigned char lds[kBLdsBytes];
     unsigned char* xs = lds;
@@ -164,6 +178,33 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     for (int c0 = 0; c0 < a.Cp; c0 += kBCC) {
         __syncthreads();  // the previous chunk is done with the staging area and V
         // -- stage the chunk's input rows --
+        if constexpr (kNhwc) {
+            // units (row r, pixel pc, 8-channel group g), 8 loads in flight per thread
+            const int nunits = rows_st * a.cols * 4;
+            _Float16* xh = reinterpret_cast<_Float16*>(xs);
+            for (int e0 = 0; e0 < nunits; e0 += 8 * kBT) {
+                u4 v[8];
+                int dst[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int e = e0 + tid + u * kBT;
+                    const int g = e & 3, rp = e >> 2;
+                    const int r = rp / a.cols, pc = rp - (rp / a.cols) * a.cols;
+                    const int h = h_first + r, w = pc - a.pad, cg = c0 + 8 * g;
+                    const bool live = e < nunits;
+                    const bool ok = live && h >= 0 && h < a.H && w >= 0 && w < a.W && cg < a.C;
+                    v[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                        xrs, ok ? 2 * (((b * a.H + h) * a.W + w) * a.C + cg) : kBOob, 0, 0);
+                    dst[u] = live ? (r * a.cols + pc) * kNhwcPix + 8 * g : -1;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (dst[u] >= 0) {  // 8-byte aligned: two 8-byte writes
+                        *reinterpret_cast<u2*>(xh + dst[u]) = u2{v[u][0], v[u][1]};
+                        *reinterpret_cast<u2*>(xh + dst[u] + 4) = u2{v[u][2], v[u][3]};
+                    }
+            }
+        } else
         for (int sp0 = 0; sp0 < nspans; sp0 += kSpr * kBT) {
             u4 v[kSpr][NJ];
             int dst[kSpr];
@@ -191,7 +232,26 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
         }
         __syncthreads();
         // -- input transform of (channel c0 + ct, tile t) into V --
-        {
+        if constexpr (kNhwc) {
+            const _Float16* src = reinterpret_cast<const _Float16*>(xs) +
+                                  ((6 * (th - th_first)) * a.cols + 6 * tw) * kNhwcPix + ct;
+            const int rstride = a.cols * kNhwcPix;
+            // the whole patch into registers first: the V writes below could
+            // alias the staging area for the compiler, which would re-read it
+            // (packed in pairs, as the NCHW form holds it)
+            h2 d[8][4];
+#pragma unroll
+            for (int ii = 0; ii < 8; ii++) {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    d[ii][q] = h2{src[ii * rstride + 2 * q * kNhwcPix],
+                                  src[ii * rstride + (2 * q + 1) * kNhwcPix]};
+                if (ii & 1) __builtin_amdgcn_sched_barrier(0);  // 16 reads in flight at most
+            }
+            input_tile_rows(
+                [&](int ii, int j) { return (float)d[ii][j >> 1][j & 1]; },
+                [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
+        } else {
             const int cg = c0 + ct;
             const unsigned char* cbase = xs + ct * a.cp + rb0;
             unsigned d4[8][4];
@@ -245,8 +305,8 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     }
     __syncthreads();  // staging area and V become M
 
-    // ---- M (fp16) to LDS: [kk][tile][position], one 16-byte write per
-    // (k, position row) of this lane ----
+    // ---- M (fp16) to LDS: [kk][tile][position] ([tile][kk][position] for
+    // NHWC), one 16-byte write per (k, position row) of this lane ----
     _Float16* ms = reinterpret_cast<_Float16*>(lds);
     {
         const int g = lane >> 4, tq = lane & 15;
@@ -258,7 +318,8 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 h8 v;
 #pragma unroll
                 for (int s = 0; s < 8; s++) v[s] = to_f16(acc[s][kb][i]);
-                *reinterpret_cast<h8*>(ms + (kk * 16 + tq) * kBMPitch + 8 * wave) = v;
+                const int mo = kNhwc ? tq * kNhwcTileP + kk * kBMPitch : (kk * 16 + tq) * kBMPitch;
+                *reinterpret_cast<h8*>(ms + mo + 8 * wave) = v;
             }
     }
     __syncthreads();
@@ -268,6 +329,41 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     const _Float16* res = a.residual;
     const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
     const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
+    if constexpr (kNhwc) {
+        // lanes over channels: pair e = (tile e / 64, channel e % 64)
+        for (int e = tid; e < 64 * 16; e += kBT) {
+            const int kk = e & 63, to = e >> 6;
+            const int k = k0 + kk;
+            if (to >= ntiles || k >= a.K) continue;
+            h8 mv[8];
+#pragma unroll
+            for (int ii = 0; ii < 8; ii++)
+                mv[ii] = *reinterpret_cast<const h8*>(ms + to * kNhwcTileP + kk * kBMPitch + 8 * ii);
+            float out[6][6];
+            output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
+            const int tlo = t0 + to;
+            const int oh = (tlo / a.nw) * 6, ow = (tlo - (tlo / a.nw) * a.nw) * 6;
+#pragma unroll
+            for (int r = 0; r < 6; r++) {
+                if (oh + r >= a.Ho) break;
+#pragma unroll
+                for (int s = 0; s < 6; s++)
+                    if (ow + s < a.Wo) {
+                        const int off = 2 * (((b * a.Ho + oh + r) * a.Wo + ow + s) * a.K + k);
+                        _Float16 v = epilogue(out[r][s], a.bias, k, relu0);
+                        if (res)
+                            v = add_residual(
+                                v,
+                                __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
+                                                                 rrs, off, 0, 0)),
+                                a.relu);
+                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
+                                                              off, 0, 0);
+                    }
+            }
+        }
+        return;
+    }
     for (int e = tid; e < 64 * 16; e += kBT) {
         const int kk = e >> 4;
         const int k = k0 + kk;
@@ -324,7 +420,7 @@ int round16i(int v) { return (v + 15) & ~15; }
 }  // namespace
 
 bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
-                      FusedBlockPlan* p) {
+                      FusedBlockPlan* p, bool nhwc) {
     (void)Cp;
     if (B < 1 || C < 1 || K < 1) return false;
     const int P = nh * nw;
@@ -335,14 +431,24 @@ bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
         maxrows = std::max(maxrows, (t0 + n - 1) / nw - t0 / nw + 1);
     }
     const int rows_st = 6 * maxrows + 2;
-    const int rp = round16i(2 * (6 * nw + 2) + 18);
-    const int cp = rows_st * rp + 16;
-    if (kBCC * cp > kBXBytes || rp / 16 > 10) return false;
+    p->nhwc = nhwc;
+    if (nhwc) {
+        // [row][pixel][channel] staging; 16-byte channel groups need C % 8 == 0
+        const int cols = 6 * nw + 2;
+        if (C % 8 != 0 || rows_st * cols * kNhwcPix * 2 > kBXBytes) return false;
+        p->cols = cols;
+        p->rp = p->cp = p->nj = 0;
+    } else {
+        const int rp = round16i(2 * (6 * nw + 2) + 18);
+        const int cp = rows_st * rp + 16;
+        if (kBCC * cp > kBXBytes || rp / 16 > 10) return false;
+        p->cols = 0;
+        p->rp = rp;
+        p->cp = cp;
+        p->nj = rp / 16;
+    }
     p->nruns = nruns;
     p->n_kblk = (K + 63) / 64;
-    p->rp = rp;
-    p->cp = cp;
-    p->nj = rp / 16;
     p->grid = (int64_t)B * nruns * p->n_kblk;
     (void)H;
     (void)W;
@@ -388,17 +494,23 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
                      0)
                     ? 1
                     : 0;
+    a.cols = p.cols;
     const dim3 grid((unsigned)p.grid), block(kBT);
+    if (p.nhwc) {
+        if (a.xd != 0) return hipErrorInvalidValue;  // 16-byte loads need an aligned x
+        fused_block_kernel<0, true><<<grid, block, 0, s>>>(a);
+        return hipGetLastError();
+    }
     switch (p.nj) {
-        case 2: fused_block_kernel<2><<<grid, block, 0, s>>>(a); break;
-        case 3: fused_block_kernel<3><<<grid, block, 0, s>>>(a); break;
-        case 4: fused_block_kernel<4><<<grid, block, 0, s>>>(a); break;
-        case 5: fused_block_kernel<5><<<grid, block, 0, s>>>(a); break;
-        case 6: fused_block_kernel<6><<<grid, block, 0, s>>>(a); break;
-        case 7: fused_block_kernel<7><<<grid, block, 0, s>>>(a); break;
-        case 8: fused_block_kernel<8><<<grid, block, 0, s>>>(a); break;
-        case 9: fused_block_kernel<9><<<grid, block, 0, s>>>(a); break;
-        case 10: fused_block_kernel<10><<<grid, block, 0, s>>>(a); break;
+        case 2: fused_block_kernel<2, false><<<grid, block, 0, s>>>(a); break;
+        case 3: fused_block_kernel<3, false><<<grid, block, 0, s>>>(a); break;
+        case 4: fused_block_kernel<4, false><<<grid, block, 0, s>>>(a); break;
+        case 5: fused_block_kernel<5, false><<<grid, block, 0, s>>>(a); break;
+        case 6: fused_block_kernel<6, false><<<grid, block, 0, s>>>(a); break;
+        case 7: fused_block_kernel<7, false><<<grid, block, 0, s>>>(a); break;
+        case 8: fused_block_kernel<8, false><<<grid, block, 0, s>>>(a); break;
+        case 9: fused_block_kernel<9, false><<<grid, block, 0, s>>>(a); break;
+        case 10: fused_block_kernel<10, false><<<grid, block, 0, s>>>(a); break;
         default: return hipErrorInvalidConfiguration;
     }
     return hipGetLastError();

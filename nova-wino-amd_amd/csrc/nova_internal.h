@@ -99,10 +99,12 @@ hipError_t launch_fused(const uint16_t* x, const uint16_t* U, uint16_t* y, uint1
 // workgroup, no scratch): layers with few channels at batch > 1.
 struct FusedBlockPlan {
     int nruns, n_kblk, rp, cp, nj;
+    int cols;   // NHWC: staged pixels per row
+    bool nhwc;  // x and y channels-last
     int64_t grid;
 };
 bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
-                      FusedBlockPlan* p);
+                      FusedBlockPlan* p, bool nhwc = false);
 hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
                               int Wo, const FusedBlockPlan& p, hipStream_t s,

@@ -2,10 +2,12 @@
 reference): for every shape class -- lane-parallel transforms (small
 problems), tile-block NHWC transforms (large ones), C not a multiple of 8 and
 an x that is not 16-byte aligned (lane-parallel fallback), odd output widths,
-pad 0 and 2 -- the NHWC forward must equal the NCHW three-pass forward bit for
-bit, in the other memory format; likewise with the bias/residual/ReLU
-epilogue, through the module (channels_last in, channels_last out) and the
-functional API. The NCHW path is itself parity-tested against the oracle.
+pad 0 and 2 -- the NHWC forward must equal the NCHW forward of the same path
+bit for bit, in the other memory format: three-pass against three-pass, and
+the fused tile-block kernel (forced, and chosen automatically at conv2_x
+B=32) against its NCHW form. Likewise with the bias/residual/ReLU epilogue,
+through the module (channels_last in, channels_last out) and the functional
+API. The NCHW paths are themselves parity-tested against the oracle.
 """
 
 import pytest
@@ -72,6 +74,44 @@ def test_nhwc_equals_nchw(B, C, K, H, pad):
     assert torch.equal(y_e, torch.relu(yb_ref + res))
 
 
+@pytest.mark.parametrize("B,C,K,H,pad", CASES + [(32, 64, 64, 56, 1), (2, 64, 64, 64, 1)])
+def test_nhwc_fused_block_equals_nchw(B, C, K, H, pad):
+    """Forced tile-block fused path: NHWC equals NCHW bit for bit (same
+    transforms, same 16-channel MFMA steps), with and without the epilogue.
+    Out of the NHWC envelope (C % 8 != 0) it runs three-pass and reports it."""
+    from nova_winograd.ops import check
+
+    print(f"[nhwc fused] B={B} C={C} K={K} H={H} pad={pad}", flush=True)
+    torch.manual_seed(16)
+    x = torch.randn(B, C, H, H, device=DEV).half()
+    w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
+    xc = x.contiguous(memory_format=CL)
+    if C % 8 != 0:
+        with pytest.raises(RuntimeError, match="fused path unsupported"):
+            _run(xc, w, pad, True, path=3)
+        check()
+        return
+    y, took = _run(xc, w, pad, True, path=3)
+    assert took == 3
+    assert y.is_contiguous(memory_format=CL)
+    y_ref, took_ref = _run(x, w, pad, False, path=0 if H > 60 else 3)
+    if took_ref != 3:  # wider than the NCHW kernel's staging: compare with three-pass
+        a, b = y.float(), y_ref.float()
+        assert ((a - b).norm() / b.norm()).item() <= 2e-3
+        assert (a - b).abs().max().item() <= 0.1
+    else:
+        assert torch.equal(y, y_ref)
+    assert torch.isfinite(y).all()
+    bias = (torch.randn(K, device=DEV) * 0.5).half()
+    res = torch.randn_like(y).contiguous(memory_format=CL)
+    y_e, _ = _run(xc, w, pad, True, bias=bias, relu=1, res=res, path=3)
+    yb, _ = _run(xc, w, pad, True, bias=bias, path=3)
+    assert torch.equal(y_e, torch.relu(yb + res))
+    ya, took_a = _run(xc, w, pad, True)
+    if took_a == 3:
+        assert torch.equal(ya, y)
+
+
 def test_nhwc_unaligned_input():
     torch.manual_seed(13)
     B, C, K, H = 8, 64, 64, 56
@@ -85,6 +125,13 @@ def test_nhwc_unaligned_input():
     assert x_cl.is_contiguous(memory_format=CL) and x_cl.data_ptr() % 16 != 0
     y, _ = _run(x_cl, w, 1, True)
     assert torch.equal(y, y_ref)
+    # the tile-block fused kernel stages with 16-byte loads: a forced fused
+    # path runs three-pass for this x and reports it
+    from nova_winograd.ops import check
+
+    with pytest.raises(RuntimeError, match="fused path unsupported"):
+        _run(x_cl, w, 1, True, path=3)
+    check()
 
 
 def test_module_and_functional_channels_last():
