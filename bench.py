@@ -151,8 +151,9 @@ KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_
                                              "output_nhwc_kernel")}
 
 NOVA_KERNELS = ["input_transform_kernel", "output_transform_kernel",
-                "wgemm_kernel<1, 1, 4, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2>",
-                "wgemm_lds_kernel<128, 128, 2, 2>", "fused_block_kernel", "fused_kernel<1>",
+                "wgemm_kernel<1, 1, 4, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2, 1>",
+                "wgemm_lds_kernel<64, 64, 2, 2, 2>", "wgemm_lds_kernel<128, 128, 2, 2, 1>",
+                "fused_block_kernel", "fused_kernel<1>",
                 "fused_kernel<2>", "fused_kernel<4>"]
 
 

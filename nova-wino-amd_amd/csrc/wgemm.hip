@@ -312,19 +312,23 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 }
 
 // Kernel per shape: register-direct 64 x 16 for GEMV-like B=1 deep layers
-// (few tiles), LDS-tiled otherwise -- 128 x 128 when both K and BP are large,
-// 64 x 64 when either is small.
+// (few tiles), LDS-tiled otherwise -- 128 x 128 only for K >= 512 with many
+// tiles, else 64 x 64, with two channel stages in flight once there are 128
+// tiles or more. Measured on MI355X (kernel replay, us): ResNet-50 at batch
+// 32, 128@28^2 9.7 -> 9.3 and 256@14^2 11.2 -> 10.4 with 64 x 64 (two stages)
+// instead of 128 x 128; 512@7^2 at batch 128 31.3 (128 x 128) vs 39.2; the
+// second stage in flight costs 0.1-0.5 us below 128 tiles.
 static int wgemm_cfg(int K, int BP) {
     if (BP <= 16) return 0;
-    if (K >= 128 && BP >= 128) return 2;
-    return 1;
+    if (K >= 512 && BP >= 128) return 2;
+    return BP >= 128 ? 3 : 1;
 }
 
 const char* wgemm_name(int K, int Cp, int BP) {
     (void)Cp;
-    static const char* names[] = {"wgemm_kernel<1, 1, 4, 1, 4>",
-                                  "wgemm_lds_kernel<64, 64, 2, 2>",
-                                  "wgemm_lds_kernel<128, 128, 2, 2>"};
+    static const char* names[] = {"wgemm_kernel<1, 1, 4, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2, 1>",
+                                  "wgemm_lds_kernel<128, 128, 2, 2, 1>",
+                                  "wgemm_lds_kernel<64, 64, 2, 2, 2>"};
     return names[wgemm_cfg(K, BP)];
 }
 
@@ -333,7 +337,8 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
     switch (wgemm_cfg(K, BP)) {
         case 0: return launch_cfg<1, 1, 4, 1, 4>(U, V, M, K, Cp, BP, s);
         case 1: return launch_lds<64, 64, 2, 2, 1>(U, V, M, K, Cp, BP, s);
-        default: return launch_lds<128, 128, 2, 2, 1>(U, V, M, K, Cp, BP, s);
+        case 2: return launch_lds<128, 128, 2, 2, 1>(U, V, M, K, Cp, BP, s);
+        default: return launch_lds<64, 64, 2, 2, 2>(U, V, M, K, Cp, BP, s);
     }
 }
 
