@@ -28,6 +28,7 @@ w Kaiming-normal (fan_in, relu) fp32, no bias.
 """
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -143,18 +144,19 @@ def pmc_workload(runs, reps, torch):
     torch.cuda.synchronize()
 
 
-# Kernel families: the library reports one name per pipeline stage; the
-# lane-parallel and channels-last forms belong to the stage's family.
+# Kernel families, one per pipeline stage: the tile-block, lane-parallel and
+# channels-last forms of a transform, and every tile configuration of the
+# GEMM, belong to their stage's family. The roofline's dominant kernel is the
+# family with the largest summed time per step.
 KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_kernel",
                                             "input_nhwc_kernel"),
+                 "wgemm": ("wgemm_kernel", "wgemm_lds_kernel"),
                  "output_transform_kernel": ("output_transform_kernel", "output_lp_kernel",
                                              "output_nhwc_kernel")}
+FAMILY_OF_KIND = {0: "input_transform_kernel", 1: "wgemm", 2: "output_transform_kernel"}
 
-NOVA_KERNELS = ["input_transform_kernel", "output_transform_kernel",
-                "wgemm_kernel<1, 1, 4, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2, 1>",
-                "wgemm_lds_kernel<64, 64, 2, 2, 2>", "wgemm_lds_kernel<128, 128, 2, 2, 1>",
-                "fused_block_kernel", "fused_kernel<1>",
-                "fused_kernel<2>", "fused_kernel<4>"]
+NOVA_KERNELS = ["input_transform_kernel", "wgemm", "output_transform_kernel",
+                "fused_block_kernel", "fused_kernel<1>", "fused_kernel<2>", "fused_kernel<4>"]
 
 
 def _name_keys(name):
@@ -233,6 +235,86 @@ def traffic_from(fetch_dir, write_dir, out_path):
     write_traffic_summary(data, os.path.join(os.path.dirname(out_path),
                                              "traffic_resnet50_3x3s1_b1_b32.md"))
     print(json.dumps(data))
+
+
+def kernel_stats_from(trace_dir, bench_json, out_path):
+    """Markdown summary of a `rocprofv3 --kernel-trace --stats --output-format
+    csv` run of bench.py: the --stats table, the library's kernels per launch
+    grid, and the agreement of each kernel family's mean duration in the trace
+    with the unprofiled bench line (bench_json: a file holding that line)."""
+    import csv
+    import glob
+
+    def one(pattern):
+        files = sorted(glob.glob(os.path.join(trace_dir, "**", pattern), recursive=True))
+        if not files:
+            raise SystemExit(f"no {pattern} under {trace_dir}")
+        with open(files[-1]) as f:
+            return list(csv.DictReader(f))
+
+    stats, trace = one("*kernel_stats.csv"), one("*kernel_trace.csv")
+    with open(bench_json) as f:
+        line = json.loads([ln for ln in f if ln.startswith("{")][-1])
+    short = lambda n, k=72: (n[:k] + "…") if len(n) > k else n  # noqa: E731
+    lines = [
+        "# Library kernels, ResNet-50 3x3 s1 layers at B=1 and B=32 (bench.py default workload)",
+        "",
+        "Commands (from the repository root, on one MI355X):",
+        "",
+        "```",
+        "python3 -u bench.py --no-extra > gpurun_out/bench_line.json",
+        "cd /tmp && export TMPDIR=/tmp && cd - && rocprofv3 --kernel-trace --stats "
+        "--output-format csv -d gpurun_out/prof_bench -o bench -- python3 -u bench.py "
+        "--no-extra --no-cpu",
+        "python3 bench.py --kernel-stats-from gpurun_out/prof_bench gpurun_out/bench_line.json"
+        "   # -> this file",
+        "```",
+        "",
+        "## rocprofv3 --stats (kernel_stats.csv), all kernels of the run",
+        "",
+        "| kernel | calls | avg us | min us | max us | % time |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    for r in stats[:20]:
+        lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.3f} | "
+                     f"{float(r['MinNs']) / 1e3:.3f} | {float(r['MaxNs']) / 1e3:.3f} | "
+                     f"{float(r['Percentage']):.2f} |")
+    lines += ["", "## Library kernels per launch grid (kernel_trace.csv, End - Start)", "",
+              "| kernel | grid (threads) | calls | mean us | median us |",
+              "|---|---:|---:|---:|---:|"]
+    groups = {}
+    for r in trace:
+        if "nova" not in r["Kernel_Name"]:
+            continue
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    for (name, grid), v in sorted(groups.items()):
+        lines.append(f"| `{short(name, 60)}` | {grid} | {len(v)} | {statistics.mean(v):.3f} | "
+                     f"{statistics.median(v):.3f} |")
+    lines += ["", "## Agreement with the bench line", "",
+              "The bench line's per-family times are hipEvents recorded by each kernel's own "
+              "dispatch packet over a timed region of the unprofiled run (first command); the "
+              "trace's are End - Start of every launch of the family in the profiled run "
+              "(call-weighted over the step's layers, as the bench averages them).", "",
+              "| family | bench avg_launch_us | rocprofv3 mean us | calls | ratio |",
+              "|---|---:|---:|---:|---:|"]
+    fams = line.get("kernel_families", {})
+    for fam, rec in fams.items():
+        keys = KERNEL_FAMILY.get(fam, (fam,))
+        d = [v for (name, _), vs in groups.items() for v in vs if any(k in name for k in keys)]
+        if not d:
+            continue
+        m = statistics.mean(d)
+        lines.append(f"| {fam} | {rec['avg_launch_us']:.3f} | {m:.3f} | {len(d)} | "
+                     f"{rec['avg_launch_us'] / m:.3f} |")
+    rl = line["roofline"]
+    lines += ["", f"Dominant family in the bench line: `{rl['kernel']}`, avg_launch_us = "
+                  f"{rl['avg_launch_us']}, achieved {rl['achieved']} GB/s = {rl['frac']} of "
+                  f"{rl['peak']} GB/s (bench value {line['value']} TFLOP/s, "
+                  f"{line['ms_per_step']} ms per step)."]
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print(f"wrote {out_path}")
 
 
 def write_traffic_summary(data, path):
@@ -458,10 +540,17 @@ def main():
                          "ResNet-50, cold-cache layer times)")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="short run for rocprofv3 --pmc passes (copy calibration + forwards)")
+    ap.add_argument("--kernel-stats-from", nargs=2, metavar=("TRACE_DIR", "BENCH_JSON"),
+                    help="write profiles/kernels_resnet50_3x3s1_b1_b32.md from a rocprofv3 "
+                         "kernel-trace run and the unprofiled bench line")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two --pmc-mode profiles into profiles/traffic.json and exit")
     args = ap.parse_args()
 
+    if args.kernel_stats_from:
+        kernel_stats_from(args.kernel_stats_from[0], args.kernel_stats_from[1],
+                          os.path.join(ROOT, "profiles", "kernels_resnet50_3x3s1_b1_b32.md"))
+        return
     if args.traffic_from:
         traffic_from(args.traffic_from[0], args.traffic_from[1],
                      os.path.join(ROOT, "profiles", "traffic.json"))
@@ -531,11 +620,30 @@ def main():
         ms_per_step = (t1 - t0) * 1e3 / args.steps
         value = total_flops / (ms_per_step * 1e-3) / 1e12
 
-        # ---- per-kernel timing: each kernel of each layer's forward is
-        # re-launched back to back by the library (nova_profile_replay) with one
-        # hipEvent pair on its own stream around the loop -> mean launch time.
-        # (Event pairs around single launches would add the command processor's
-        # per-packet overhead to short kernels.)
+        # ---- per-kernel durations over a timed region: the same K steps
+        # again, every kernel of every forward timed by a pair of hipEvents
+        # that its own dispatch packet records on the library's stream
+        # (nova_profile_enable: hipExtLaunchKernelGGL start/stop events), i.e.
+        # the kernel's execution without the dispatch gap in front of it.
+        for r in runs:
+            lib.nova_profile_enable(r["mod"]._handle.h, 1)
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        tot = (ctypes.c_double * 4)()
+        cnt = (ctypes.c_longlong * 4)()
+        for r in runs:
+            h = r["mod"]._handle.h
+            if lib.nova_profile_read(h, tot, cnt) < 0:
+                raise RuntimeError(lib.nova_get_last_error_message().decode())
+            lib.nova_profile_enable(h, 0)
+            r["event"] = {k: tot[k] / cnt[k] for k in range(4) if cnt[k] > 0}
+
+        # ---- cross-check: each kernel of each layer's forward re-launched
+        # back to back by the library (nova_profile_replay), one hipEvent pair
+        # on its stream around the loop -> mean launch time without the
+        # dependent-launch gap.
         kernels = {}
         for r in runs:
             y_keep = r["mod"](r["x"])  # the forward whose launches are replayed
@@ -543,19 +651,23 @@ def main():
             r["kernels"] = {}
             for k in range(4):
                 kname = lib.nova_profile_kernel_name(h, k).decode()
-                if not kname:
+                if not kname or k not in r["event"]:
                     continue
                 per = lib.nova_profile_replay(h, k, args.kernel_reps)
                 if per < 0:
                     lib.nova_get_last_error()  # kind not launched by this path
                     continue
+                ev = r["event"][k]
                 ab = kernel_alg_bytes(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"])
-                r["kernels"][KIND_NAMES[k]] = {"kernel": kname, "avg_us": per * 1e3,
-                                              "alg_bytes": ab,
-                                              "gbs": ab / (per * 1e-3) / 1e9}
-                agg = kernels.setdefault(kname, {"ms": 0.0, "launches": 0, "bytes": 0.0,
-                                                 "by_layer": []})
-                agg["ms"] += per
+                r["kernels"][KIND_NAMES[k]] = {"kernel": kname, "avg_us": ev * 1e3,
+                                              "replay_us": per * 1e3, "alg_bytes": ab,
+                                              "gbs": ab / (ev * 1e-3) / 1e9}
+                fam = FAMILY_OF_KIND.get(k, kname)
+                agg = kernels.setdefault(fam, {"ms": 0.0, "replay_ms": 0.0, "launches": 0,
+                                               "bytes": 0.0, "by_layer": [], "members": {}})
+                agg["members"][kname] = agg["members"].get(kname, 0) + 1
+                agg["ms"] += ev
+                agg["replay_ms"] += per
                 agg["launches"] += 1
                 agg["bytes"] += ab
                 agg["by_layer"].append(f"{r['name']}_b{r['B']}")
@@ -593,11 +705,22 @@ def main():
         "traffic": load_traffic(dom_name),
         "kernel": dom_name,
         "avg_launch_us": round(avg_s * 1e6, 3),
+        "timing": "hipEvents recorded by each kernel's dispatch packet over a timed region of K steps",
+        "replay_avg_launch_us": round(dom["replay_ms"] / dom["launches"] * 1e3, 3),
+        "members": dom["members"],
         "alg_bytes_per_launch": round(bytes_per_launch),
         "launches_per_step": dom["launches"],
         "share_of_kernel_time": round(dom["ms"] / sum(v["ms"] for v in kernels.values()), 3),
         "layers": dom_desc,
     }
+
+    families = {
+        fam: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 3),
+              "launches_per_step": v["launches"],
+              "ms_per_step": round(v["ms"], 4),
+              "achieved_gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
+              "frac_hbm": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        for fam, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])}
 
     layers_out = []
     for r in runs:
@@ -660,6 +783,7 @@ def main():
             "interface": "NovaWinogradConv2d module (ctypes C-ABI), eager",
         },
         "roofline": roofline,
+        "kernel_families": families,
         "cpu_baseline": cpu,
         "layers": layers_out,
     }

@@ -153,11 +153,14 @@ NOVA_API int nova_get_last_path(nova_handle_t h);
 /* Internal workspace bytes a forward of this shape needs on this handle. */
 NOVA_API long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad);
 
-/* Per-kernel timing for measurement. enable != 0 records hipEvents on the
- * handle's stream around each kernel of every forward (at most 4096 forwards
- * between reads); nova_profile_read() waits for them, writes the total ms and
- * launch count per kernel kind (0 input transform, 1 GEMM, 2 output
- * transform, 3 fused) and resets. Returns the number of timed launches. */
+/* Per-kernel timing for measurement. enable != 0 times each kernel of every
+ * forward on the handle with a pair of hipEvents that the kernel's own
+ * dispatch packet records (hipExtLaunchKernelGGL start/stop events), so the
+ * interval is the kernel's execution alone (at most 4096 three-kernel
+ * forwards between reads); nova_profile_read() waits for them, writes the
+ * total ms and launch count per kernel kind (0 input transform, 1 GEMM,
+ * 2 output transform, 3 fused) and resets. Returns the number of timed
+ * launches. */
 NOVA_API void nova_profile_enable(nova_handle_t h, int enable);
 NOVA_API int nova_profile_read(nova_handle_t h, double* total_ms, long long* count);
 /* Re-launches the kernel of `kind` from the handle's most recent forward

@@ -20,6 +20,11 @@
 
 namespace nova {
 
+KernelEvents& kernel_events() {
+    static thread_local KernelEvents ev;
+    return ev;
+}
+
 static thread_local int g_err = 0;
 static thread_local char g_msg[512] = "";
 
@@ -38,9 +43,12 @@ constexpr uint32_t kMagic = 0x4e4f5641u;  // "NOVA"
 // Kernel kinds for per-kernel timing.
 enum Kind { kKindInput = 0, kKindGemm = 1, kKindOutput = 2, kKindFused = 3, kNumKinds = 4 };
 
-// Optional per-kernel timing: hipEvents recorded on the handle's stream
-// around every kernel a forward launches. Off by default (zero overhead).
+// Optional per-kernel timing: every kernel a forward launches records its own
+// start and end into a pair of hipEvents (its dispatch packet's timestamps,
+// see KernelEvents), so a pair times the kernel alone. Off by default (zero
+// overhead); the event pool grows on demand up to kMaxEvents.
 struct Profiler {
+    static constexpr size_t kMaxEvents = 2 * 3 * 4096;  // 4096 three-kernel forwards
     bool on = false;
     std::vector<hipEvent_t> pool;
     size_t next = 0;
@@ -53,16 +61,35 @@ struct Profiler {
     // last launch of each kind (first sub-batch), re-issued by replay()
     std::function<hipError_t()> last[kNumKinds];
 
-    // Returns the index of a recorded event, or SIZE_MAX when disabled/exhausted.
-    size_t mark(hipStream_t s) {
-        if (!on || next >= pool.size()) return SIZE_MAX;
-        if (hipEventRecord(pool[next], s) != hipSuccess) return SIZE_MAX;
-        return next++;
+    bool grow() {
+        const size_t want = std::min(kMaxEvents, std::max<size_t>(64, 2 * pool.size()));
+        while (pool.size() < want) {
+            hipEvent_t e;
+            if (hipEventCreate(&e) != hipSuccess) return false;
+            pool.push_back(e);
+        }
+        return true;
     }
-    void span(int kind, size_t e0, size_t e1, const char* name) {
-        if (e0 == SIZE_MAX || e1 == SIZE_MAX) return;
-        spans.push_back({kind, e0, e1});
+    // Arms the calling thread's kernel events for the next launch; returns the
+    // index of the start event, or SIZE_MAX when disabled or exhausted.
+    size_t arm() {
+        if (!on) return SIZE_MAX;
+        if (next + 2 > pool.size() && (pool.size() >= kMaxEvents || !grow())) return SIZE_MAX;
+        if (next + 2 > pool.size()) return SIZE_MAX;
+        kernel_events() = KernelEvents{pool[next], pool[next + 1]};
+        next += 2;
+        return next - 2;
+    }
+    // After the launch: records the kernel's name for its kind and keeps the
+    // span if the kernel took the events.
+    void done(int kind, size_t e0, const char* name) {
         names[kind] = name;
+        if (e0 == SIZE_MAX) return;
+        if (kernel_events().start != nullptr) {  // nothing was launched
+            kernel_events() = KernelEvents{};
+            return;
+        }
+        spans.push_back({kind, e0, e0 + 1});
     }
 };
 
@@ -264,20 +291,18 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
         pf.last[kKindOutput] = out;
         pf.last[kKindFused] = nullptr;
     }
-    const size_t e0 = pf.mark(st);
-    if (!hip_ok(in(), "input transform")) return false;
-    const size_t e1 = pf.mark(st);
-    if (!hip_ok(gm(), "wgemm")) return false;
-    const size_t e2 = pf.mark(st);
-    if (!hip_ok(out(), "output transform")) return false;
-    const size_t e3 = pf.mark(Hd->stream);
-    pf.names[kKindInput] = "input_transform_kernel";
-    pf.names[kKindGemm] = wgemm_name(K, Cp, (int)s.BP);
-    pf.names[kKindOutput] = "output_transform_kernel";
-    pf.span(kKindInput, e0, e1, pf.names[kKindInput]);
-    pf.span(kKindGemm, e1, e2, pf.names[kKindGemm]);
-    pf.span(kKindOutput, e2, e3, pf.names[kKindOutput]);
-    return true;
+    size_t e = pf.arm();
+    const bool ok_in = hip_ok(in(), "input transform");
+    pf.done(kKindInput, e, "input_transform_kernel");
+    if (!ok_in) return false;
+    e = pf.arm();
+    const bool ok_gm = hip_ok(gm(), "wgemm");
+    pf.done(kKindGemm, e, wgemm_name(K, Cp, (int)s.BP));
+    if (!ok_gm) return false;
+    e = pf.arm();
+    const bool ok_out = hip_ok(out(), "output transform");
+    pf.done(kKindOutput, e, "output_transform_kernel");
+    return ok_out;
 }
 
 // Core forward. V_user/M_user may be null; caps are in fp16 elements.
@@ -359,10 +384,10 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
                 pf.last[kKindFused] = fz;
             }
-            pf.names[kKindFused] = "fused_block_kernel";
-            const size_t e0 = pf.mark(st);
-            if (!hip_ok(fz(), "fused block kernel")) return;
-            pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
+            const size_t e0 = pf.arm();
+            const bool ok = hip_ok(fz(), "fused block kernel");
+            pf.done(kKindFused, e0, "fused_block_kernel");
+            if (!ok) return;
         } else if (path == 2) {
             const hipStream_t st = Hd->stream;
             const uint16_t* U = Hd->Uf;
@@ -384,10 +409,10 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
                 pf.last[kKindFused] = fz;
             }
-            pf.names[kKindFused] = fused_name(fp);
-            const size_t e0 = pf.mark(st);
-            if (!hip_ok(fz(), "fused kernel")) return;
-            pf.span(kKindFused, e0, pf.mark(st), pf.names[kKindFused]);
+            const size_t e0 = pf.arm();
+            const bool ok = hip_ok(fz(), "fused kernel");
+            pf.done(kKindFused, e0, fused_name(fp));
+            if (!ok) return;
         } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0, ep)) {
             return;
         }
@@ -664,14 +689,9 @@ void nova_profile_enable(nova_handle_t h, int enable) {
     Handle* H = as_handle(h, "nova_profile_enable");
     if (!H) return;
     Profiler& pf = H->prof;
-    if (enable && pf.pool.empty()) {
-        const size_t n = 4 * 4096;  // 4096 three-kernel forwards between reads
-        pf.pool.reserve(n);
-        for (size_t i = 0; i < n; i++) {
-            hipEvent_t e;
-            if (!hip_ok(hipEventCreate(&e), "hipEventCreate")) break;
-            pf.pool.push_back(e);
-        }
+    if (enable && pf.pool.empty() && !pf.grow()) {
+        set_error(kErrHip, "nova_profile_enable: hipEventCreate failed");
+        return;
     }
     pf.on = enable != 0;
     pf.next = 0;

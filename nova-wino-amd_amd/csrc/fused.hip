@@ -490,9 +490,9 @@ hipError_t launch_fused(const uint16_t* x, const uint16_t* Uf, uint16_t* y, uint
     a.nks = (Cp + 15) / 16;
     const dim3 grid((unsigned)p.grid), block(kFThreads);
     switch (p.nm) {
-        case 1: fused_kernel<1><<<grid, block, 0, s>>>(a); break;
-        case 2: fused_kernel<2><<<grid, block, 0, s>>>(a); break;
-        default: fused_kernel<4><<<grid, block, 0, s>>>(a); break;
+        case 1: launch(fused_kernel<1>, grid, block, s, a); break;
+        case 2: launch(fused_kernel<2>, grid, block, s, a); break;
+        default: launch(fused_kernel<4>, grid, block, s, a); break;
     }
     return hipGetLastError();
 }

@@ -498,19 +498,19 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     const dim3 grid((unsigned)p.grid), block(kBT);
     if (p.nhwc) {
         if (a.xd != 0) return hipErrorInvalidValue;  // 16-byte loads need an aligned x
-        fused_block_kernel<0, true><<<grid, block, 0, s>>>(a);
+        launch(fused_block_kernel<0, true>, grid, block, s, a);
         return hipGetLastError();
     }
     switch (p.nj) {
-        case 2: fused_block_kernel<2, false><<<grid, block, 0, s>>>(a); break;
-        case 3: fused_block_kernel<3, false><<<grid, block, 0, s>>>(a); break;
-        case 4: fused_block_kernel<4, false><<<grid, block, 0, s>>>(a); break;
-        case 5: fused_block_kernel<5, false><<<grid, block, 0, s>>>(a); break;
-        case 6: fused_block_kernel<6, false><<<grid, block, 0, s>>>(a); break;
-        case 7: fused_block_kernel<7, false><<<grid, block, 0, s>>>(a); break;
-        case 8: fused_block_kernel<8, false><<<grid, block, 0, s>>>(a); break;
-        case 9: fused_block_kernel<9, false><<<grid, block, 0, s>>>(a); break;
-        case 10: fused_block_kernel<10, false><<<grid, block, 0, s>>>(a); break;
+        case 2: launch(fused_block_kernel<2, false>, grid, block, s, a); break;
+        case 3: launch(fused_block_kernel<3, false>, grid, block, s, a); break;
+        case 4: launch(fused_block_kernel<4, false>, grid, block, s, a); break;
+        case 5: launch(fused_block_kernel<5, false>, grid, block, s, a); break;
+        case 6: launch(fused_block_kernel<6, false>, grid, block, s, a); break;
+        case 7: launch(fused_block_kernel<7, false>, grid, block, s, a); break;
+        case 8: launch(fused_block_kernel<8, false>, grid, block, s, a); break;
+        case 9: launch(fused_block_kernel<9, false>, grid, block, s, a); break;
+        case 10: launch(fused_block_kernel<10, false>, grid, block, s, a); break;
         default: return hipErrorInvalidConfiguration;
     }
     return hipGetLastError();

@@ -2,10 +2,37 @@
 // Nothing here is exported; the public C-ABI is include/nova_winograd.h.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <cstdint>
 
 namespace nova {
+
+// Per-kernel timing hook. When a caller sets the calling thread's
+// KernelEvents, the next kernel that thread launches records its own start
+// and end (the timestamps of its dispatch packet, hipExtLaunchKernelGGL) into
+// those events, which then time the kernel alone -- without the dispatch gap
+// in front of it that events recorded between kernels would include. The
+// events are consumed by that launch. Unset (the default), launches are plain
+// triple-chevron launches.
+struct KernelEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+KernelEvents& kernel_events();
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+                   Args... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+    KernelEvents& ev = kernel_events();
+    if (ev.start != nullptr) {
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev.start, ev.stop, 0,
+                              static_cast<KArgs>(args)...);
+        ev = KernelEvents{};
+    } else {
+        kernel<<<grid, block, 0, s>>>(static_cast<KArgs>(args)...);
+    }
+}
 
 // Error codes returned by nova_get_last_error().
 enum Status : int {

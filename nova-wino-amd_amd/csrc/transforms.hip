@@ -69,7 +69,7 @@ hipError_t launch_filter_transform_ref(const float* w, uint16_t* U, int K, int C
                                        hipStream_t s) {
     const int64_t n = (int64_t)K * C;
     const int64_t blocks = (n + 255) / 256;
-    filter_transform_kernel<true, float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+    launch(filter_transform_kernel<true, float>, dim3((unsigned)blocks), dim3(256), s,
         w, reinterpret_cast<_Float16*>(U), K, C, C);
     return hipGetLastError();
 }
@@ -79,10 +79,10 @@ hipError_t launch_filter_transform_gemm(const void* w, bool w_f16, uint16_t* U, 
     const int64_t n = (int64_t)K * Cp;
     const int64_t blocks = (n + 255) / 256;
     if (w_f16)
-        filter_transform_kernel<false, _Float16><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        launch(filter_transform_kernel<false, _Float16>, dim3((unsigned)blocks), dim3(256), s,
             static_cast<const _Float16*>(w), reinterpret_cast<_Float16*>(U), K, C, Cp);
     else
-        filter_transform_kernel<false, float><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        launch(filter_transform_kernel<false, float>, dim3((unsigned)blocks), dim3(256), s,
             static_cast<const float*>(w), reinterpret_cast<_Float16*>(U), K, C, Cp);
     return hipGetLastError();
 }
@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void u_frag_kernel(const _Float16* __restrict_
 hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStream_t s) {
     const int nkt = (K + 15) / 16, nks = (Cp + 15) / 16;
     const int64_t nslots = (int64_t)64 * nkt * nks * 64;
-    u_frag_kernel<<<dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, s>>>(
+    launch(u_frag_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), s,
         reinterpret_cast<const _Float16*>(U), reinterpret_cast<_Float16*>(Uf), K, Cp, nkt, nks,
         nslots);
     return hipGetLastError();
@@ -434,11 +434,11 @@ static hipError_t launch_input_lp(const uint16_t* x, uint16_t* V, int B, int C, 
     const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     if (nhwc)
-        input_lp_kernel<true><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+        launch(input_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
             nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
     else
-        input_lp_kernel<false><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+        launch(input_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
             nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
     return hipGetLastError();
@@ -501,13 +501,13 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
         _Float16* Vh = reinterpret_cast<_Float16*>(V);
         const dim3 grid((unsigned)nblocks), block(256);
         if (tw == 2)
-            input_nhwc_kernel<2><<<grid, block, 0, s>>>(xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
+            launch(input_nhwc_kernel<2>, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
                                                         cblocks, (int)x_bytes, 2 * 64 * pstride);
         else if (tw == 4)
-            input_nhwc_kernel<4><<<grid, block, 0, s>>>(xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
+            launch(input_nhwc_kernel<4>, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
                                                         cblocks, (int)x_bytes, 2 * 64 * pstride);
         else
-            input_nhwc_kernel<8><<<grid, block, 0, s>>>(xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
+            launch(input_nhwc_kernel<8>, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
                                                         cblocks, (int)x_bytes, 2 * 64 * pstride);
         return hipGetLastError();
     }
@@ -526,17 +526,17 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     const dim3 grid((unsigned)nblocks), block(256);
     switch (tw) {
         case 2:
-            input_transform_kernel<2><<<grid, block, 0, s>>>(xa, Vh, C, H, W, pad, nh, nw, ldv,
+            launch(input_transform_kernel<2>, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv,
                                                              pstride, cblocks, (int)x_bytes, xd,
                                                              2 * 64 * pstride);
             break;
         case 4:
-            input_transform_kernel<4><<<grid, block, 0, s>>>(xa, Vh, C, H, W, pad, nh, nw, ldv,
+            launch(input_transform_kernel<4>, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv,
                                                              pstride, cblocks, (int)x_bytes, xd,
                                                              2 * 64 * pstride);
             break;
         default:
-            input_transform_kernel<8><<<grid, block, 0, s>>>(xa, Vh, C, H, W, pad, nh, nw, ldv,
+            launch(input_transform_kernel<8>, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv,
                                                              pstride, cblocks, (int)x_bytes, xd,
                                                              2 * 64 * pstride);
             break;
@@ -740,13 +740,13 @@ static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, 
                           int relu, const _Float16* res) {
     const dim3 block(256);
     if (vw == 4)
-        output_transform_kernel<TW, 4><<<grid, block, 0, s>>>(
+        launch(output_transform_kernel<TW, 4>, grid, block, s,
             Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
     else if (vw == 2)
-        output_transform_kernel<TW, 2><<<grid, block, 0, s>>>(
+        launch(output_transform_kernel<TW, 2>, grid, block, s,
             Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
     else
-        output_transform_kernel<TW, 1><<<grid, block, 0, s>>>(
+        launch(output_transform_kernel<TW, 1>, grid, block, s,
             Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
 }
 
@@ -878,13 +878,13 @@ static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K,
                           ? 1
                           : 0;
     if (nhwc)
-        output_lp_kernel<true><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+        launch(output_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
             ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
             reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
             reinterpret_cast<const _Float16*>(ep.residual));
     else
-        output_lp_kernel<false><<<dim3((unsigned)items), dim3(256), 0, s>>>(
+        launch(output_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
             ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
             reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
@@ -911,15 +911,15 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
         const _Float16* res = reinterpret_cast<const _Float16*>(ep.residual);
         const dim3 grid((unsigned)nblocks), block(256);
         if (tw == 2)
-            output_nhwc_kernel<2><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+            launch(output_nhwc_kernel<2>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
                                                          kblocks, 2 * 64 * pstride, y_bytes, bias,
                                                          ep.relu, res);
         else if (tw == 4)
-            output_nhwc_kernel<4><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+            launch(output_nhwc_kernel<4>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
                                                          kblocks, 2 * 64 * pstride, y_bytes, bias,
                                                          ep.relu, res);
         else
-            output_nhwc_kernel<8><<<grid, block, 0, s>>>(Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
+            launch(output_nhwc_kernel<8>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
                                                          kblocks, 2 * 64 * pstride, y_bytes, bias,
                                                          ep.relu, res);
         return hipGetLastError();

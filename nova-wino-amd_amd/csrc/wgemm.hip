@@ -134,7 +134,7 @@ static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, 
                              int BP, hipStream_t s) {
     constexpr int TM = MT * 16 * WGM, TN = NT * 16 * WGN;
     dim3 grid((unsigned)((BP + TN - 1) / TN), (unsigned)((K + TM - 1) / TM), 64);
-    wgemm_kernel<MT, NT, WGM, WGN, PD><<<grid, dim3(64 * WGM * WGN), 0, s>>>(
+    launch(wgemm_kernel<MT, NT, WGM, WGN, PD>, grid, dim3(64 * WGM * WGN), s,
         reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
         reinterpret_cast<_Float16*>(M), K, Cp, BP);
     return hipGetLastError();
@@ -305,7 +305,7 @@ template <int TK, int TB, int WK, int WB, int PF>
 static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                              int BP, hipStream_t s) {
     const unsigned grid = 64u * (unsigned)((BP + TB - 1) / TB) * (unsigned)((K + TK - 1) / TK);
-    wgemm_lds_kernel<TK, TB, WK, WB, PF><<<dim3(grid), dim3(256), 0, s>>>(
+    launch(wgemm_lds_kernel<TK, TB, WK, WB, PF>, dim3(grid), dim3(256), s,
         reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
         reinterpret_cast<_Float16*>(M), K, Cp, BP);
     return hipGetLastError();
