@@ -276,9 +276,10 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
     const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
     const uint16_t* U = Hd->U;
     const bool nhwc = Hd->nhwc != 0;
+    const bool stream_v = wgemm_v_reads(K, (int)s.BP) <= 4;
     auto in = [=]() {
         return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp,
-                                      (int64_t)Cp * s.BP, st, nhwc);
+                                      (int64_t)Cp * s.BP, st, nhwc, stream_v);
     };
     auto gm = [=]() { return launch_wgemm(U, V, M, K, Cp, (int)s.BP, st); };
     auto out = [=]() {

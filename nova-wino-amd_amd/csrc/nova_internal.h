@@ -82,9 +82,11 @@ hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStre
 // ---- input transform -----------------------------------------------------
 // V[p*pstride + bp*ldv + c], bp = (b*nh + th)*nw + tw, for th < nh, tw < nw.
 // Channels c in [C, ldv) are written as zero. x is NCHW, or NHWC if nhwc.
+// stream_v: the tile-block forms store V with the non-temporal (nt) cache
+// policy (results unchanged; see wgemm_v_reads for when it pays).
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s, bool nhwc = false);
+                                  hipStream_t s, bool nhwc = false, bool stream_v = false);
 
 // ---- output transform ----------------------------------------------------
 // Reads M[p*pstride + bp*ldm + k]; writes y[b][k][h][w] (y[b][h][w][k] if
@@ -99,6 +101,12 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
 // [64][BP][K].
 hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                         int BP, hipStream_t s);
+// Times the GEMM reads each V element (its output-channel tiles). Measured on
+// MI355X (whole forwards): streaming V past the L2 pays when this is at most 4
+// (ResNet-50 at batch 32: 128@28^2 31.7 -> 28.9 us, 256@14^2 31.2 -> 30.3,
+// 512@7^2 29.0 -> 28.4) and costs when V is re-read more often (320@128^2 at
+// batch 1, five reads: 43.1 -> 45.1 us; 640@64^2, ten: 36.7 -> 39.1 us).
+int wgemm_v_reads(int K, int BP);
 // Kernel name (template configuration) launch_wgemm picks for this shape.
 const char* wgemm_name(int K, int Cp, int BP);
 

@@ -124,6 +124,11 @@ hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStre
 // per-access vector address arithmetic).
 // ---------------------------------------------------------------------------
 constexpr int kOob = (int)0x80000000;  // byte offset beyond any buffer used here
+// Cache-policy operand of a buffer store that streams past the L2 (nt). The
+// tile-block input transforms write V in whole 128-byte lines (64 lanes x 2
+// bytes); streamed, V goes to the memory-side cache without filling the L2
+// with dirty lines that the kernel's end would have to write back.
+constexpr int kNt = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
@@ -163,7 +168,7 @@ struct InGeom {
     __device__ static int base(int c) { return c * kCP; }
 };
 
-template <int TW>
+template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int xd,
@@ -278,7 +283,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
         [&](int r, int s, float v) {
             const int p = r * 8 + s;
             __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, to_f16(v)), vrs,
-                                                  voff, (int)(2 * p * pstride), 0);
+                                                  voff, (int)(2 * p * pstride), kStream ? kNt : 0);
         });
 }
 
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
 // kernel. Zero padding is already in LDS, so no masks. Needs C % 8 == 0 and a
 // 16-byte aligned x (the launcher checks; otherwise the lane-parallel form).
 // ---------------------------------------------------------------------------
-template <int TW>
+template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_nhwc_kernel(
     const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int64_t v_bytes) {
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(256) void input_nhwc_kernel(
                         const int p = r * 8 + s2;
                         __builtin_amdgcn_raw_buffer_store_b16(
                             __builtin_bit_cast(uint16_t, to_f16(v)), vrs, voff,
-                            (int)(2 * p * pstride), 0);
+                            (int)(2 * p * pstride), kStream ? kNt : 0);
                     });
 }
 
@@ -485,36 +490,33 @@ static bool latency_bound(int64_t rows, int n, int ch) {
 
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s, bool nhwc) {
+                                  hipStream_t s, bool nhwc, bool stream_v) {
     if (latency_bound((int64_t)B * nh, nw, ldv) ||
         (nhwc && (C % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0)))
         return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, nhwc);
     const int tw = pick_tw((int64_t)B * nh, nw, ldv);
-    if (nhwc) {
-        const int cb = 256 / tw;
-        const int cblocks = (ldv + cb - 1) / cb;
-        const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * cblocks;
-        const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
-        if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
-        if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
-        const _Float16* xh = reinterpret_cast<const _Float16*>(x);
-        _Float16* Vh = reinterpret_cast<_Float16*>(V);
-        const dim3 grid((unsigned)nblocks), block(256);
-        if (tw == 2)
-            launch(input_nhwc_kernel<2>, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
-                                                        cblocks, (int)x_bytes, 2 * 64 * pstride);
-        else if (tw == 4)
-            launch(input_nhwc_kernel<4>, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
-                                                        cblocks, (int)x_bytes, 2 * 64 * pstride);
-        else
-            launch(input_nhwc_kernel<8>, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride,
-                                                        cblocks, (int)x_bytes, 2 * 64 * pstride);
-        return hipGetLastError();
-    }
     const int cb = 256 / tw;
     const int cblocks = (ldv + cb - 1) / cb;
     const int64_t nblocks = (int64_t)((nw + tw - 1) / tw) * nh * B * cblocks;
     if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
+    const dim3 grid((unsigned)nblocks), block(256);
+    _Float16* Vh = reinterpret_cast<_Float16*>(V);
+    if (nhwc) {
+        const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
+        if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
+        const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+        auto go = [&](auto kernel) {
+            launch(kernel, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
+                   (int)x_bytes, 2 * 64 * pstride);
+        };
+        if (tw == 2)
+            stream_v ? go(input_nhwc_kernel<2, true>) : go(input_nhwc_kernel<2, false>);
+        else if (tw == 4)
+            stream_v ? go(input_nhwc_kernel<4, true>) : go(input_nhwc_kernel<4, false>);
+        else
+            stream_v ? go(input_nhwc_kernel<8, true>) : go(input_nhwc_kernel<8, false>);
+        return hipGetLastError();
+    }
     // x is addressed from the 16-byte boundary at or below it (same granule,
     // so no byte outside x's pages is touched); offsets stay 32-bit.
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
@@ -522,25 +524,16 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     const int64_t x_bytes = 2 * (int64_t)B * C * H * W + xd;
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
-    _Float16* Vh = reinterpret_cast<_Float16*>(V);
-    const dim3 grid((unsigned)nblocks), block(256);
-    switch (tw) {
-        case 2:
-            launch(input_transform_kernel<2>, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv,
-                                                             pstride, cblocks, (int)x_bytes, xd,
-                                                             2 * 64 * pstride);
-            break;
-        case 4:
-            launch(input_transform_kernel<4>, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv,
-                                                             pstride, cblocks, (int)x_bytes, xd,
-                                                             2 * 64 * pstride);
-            break;
-        default:
-            launch(input_transform_kernel<8>, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv,
-                                                             pstride, cblocks, (int)x_bytes, xd,
-                                                             2 * 64 * pstride);
-            break;
-    }
+    auto go = [&](auto kernel) {
+        launch(kernel, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
+               (int)x_bytes, xd, 2 * 64 * pstride);
+    };
+    if (tw == 2)
+        stream_v ? go(input_transform_kernel<2, true>) : go(input_transform_kernel<2, false>);
+    else if (tw == 4)
+        stream_v ? go(input_transform_kernel<4, true>) : go(input_transform_kernel<4, false>);
+    else
+        stream_v ? go(input_transform_kernel<8, true>) : go(input_transform_kernel<8, false>);
     return hipGetLastError();
 }
 
@@ -912,16 +905,13 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
         const dim3 grid((unsigned)nblocks), block(256);
         if (tw == 2)
             launch(output_nhwc_kernel<2>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                                                         kblocks, 2 * 64 * pstride, y_bytes, bias,
-                                                         ep.relu, res);
+                   kblocks, 2 * 64 * pstride, y_bytes, bias, ep.relu, res);
         else if (tw == 4)
             launch(output_nhwc_kernel<4>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                                                         kblocks, 2 * 64 * pstride, y_bytes, bias,
-                                                         ep.relu, res);
+                   kblocks, 2 * 64 * pstride, y_bytes, bias, ep.relu, res);
         else
             launch(output_nhwc_kernel<8>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                                                         kblocks, 2 * 64 * pstride, y_bytes, bias,
-                                                         ep.relu, res);
+                   kblocks, 2 * 64 * pstride, y_bytes, bias, ep.relu, res);
         return hipGetLastError();
     }
     const _Float16* bias = reinterpret_cast<const _Float16*>(ep.bias);
