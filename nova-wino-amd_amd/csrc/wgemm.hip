@@ -152,7 +152,7 @@ static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 constexpr int kStageC = 64;
 constexpr int kPitch = 72;
 
-template <int TK, int TB, int WK, int WB, int PF>
+template <int TK, int TB, int WK, int WB, int PF, int SM>
 __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restrict__ U,
                                                         const _Float16* __restrict__ V,
                                                         _Float16* __restrict__ M, int K, int Cp,
@@ -278,6 +278,38 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
     }
 
     const int mu = 2 * p * BP * K;
+    if constexpr (SM != 0) {
+        // SM 1/2: the M tile goes through LDS as [bp][k] rows and leaves as
+        // whole rows, 16 bytes per lane (SM 2: with the nt cache policy); the
+        // L2 then holds whole dirty lines instead of 32-byte pieces of 16.
+        if ((K & 7) == 0) {
+            constexpr int kMP = TK + 8;  // halves per staged row
+            static_assert(TB * kMP <= 2 * TK * kPitch, "M tile fits in sU");
+            _Float16* sm = &sU[0][0];
+#pragma unroll
+            for (int mi = 0; mi < MT; mi++)
+#pragma unroll
+                for (int ni = 0; ni < NT; ni++) {
+                    const int bpl = (wb * NT + ni) * 16 + r16;
+                    const int kl = (wk * MT + mi) * 16 + 4 * g;
+                    *reinterpret_cast<h4*>(sm + bpl * kMP + kl) =
+                        h4{(_Float16)acc[mi][ni][0], (_Float16)acc[mi][ni][1],
+                           (_Float16)acc[mi][ni][2], (_Float16)acc[mi][ni][3]};
+                }
+            __syncthreads();
+            typedef unsigned u4 __attribute__((ext_vector_type(4)));
+            constexpr int kCh = TK / 8;  // 16-byte chunks per row
+#pragma unroll
+            for (int e = tid; e < TB * kCh; e += 256) {
+                const int row = e / kCh, ch = e % kCh;
+                const int bp = n0 + row, k = k0 + 8 * ch;
+                const u4 v = *reinterpret_cast<const u4*>(sm + row * kMP + 8 * ch);
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v, mrs, (bp < BP && k < K) ? 2 * (bp * K + k) : kOob, mu, SM == 2 ? 2 : 0);
+            }
+            return;
+        }
+    }
     const bool vec_store = (K & 3) == 0;
 #pragma unroll
     for (int mi = 0; mi < MT; mi++)
@@ -301,22 +333,40 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         }
 }
 
+// M epilogue of the LDS kernels (SM of wgemm_lds_kernel): always staged
+// through LDS as whole rows (K % 8 == 0); stored with the nt cache policy
+// when M holds 4-16 MB. Measured on MI355X, whole forwards, us (direct b64
+// stores -> staged -> staged + nt): ResNet-50 batch 32 128@28^2 28.9 -> 28.0
+// -> 27.4, 256@14^2 30.2 -> 29.6 -> 28.4, 512@7^2 28.6 -> 27.1 -> 26.7,
+// conv2_x three-pass 40.8 -> 36.4 -> 37.0; batch 128 128@28^2 70.3 -> 64.1
+// -> 68.4; batch 1 64@56^2 10.9 -> 10.4 -> 10.7. Outside 4-16 MB the nt
+// stores were as often slower as faster.
+static int m_epilogue(int K, int BP) {
+    const int64_t m_bytes = 2 * (int64_t)64 * BP * K;
+    return (m_bytes >= (4 << 20) && m_bytes <= (16 << 20)) ? 2 : 1;
+}
+
 template <int TK, int TB, int WK, int WB, int PF>
 static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, int K, int Cp,
                              int BP, hipStream_t s) {
     const unsigned grid = 64u * (unsigned)((BP + TB - 1) / TB) * (unsigned)((K + TK - 1) / TK);
-    launch(wgemm_lds_kernel<TK, TB, WK, WB, PF>, dim3(grid), dim3(256), s,
-        reinterpret_cast<const _Float16*>(U), reinterpret_cast<const _Float16*>(V),
-        reinterpret_cast<_Float16*>(M), K, Cp, BP);
+    auto go = [&](auto kernel) {
+        launch(kernel, dim3(grid), dim3(256), s, reinterpret_cast<const _Float16*>(U),
+               reinterpret_cast<const _Float16*>(V), reinterpret_cast<_Float16*>(M), K, Cp, BP);
+    };
+    if (m_epilogue(K, BP) == 2)
+        go(wgemm_lds_kernel<TK, TB, WK, WB, PF, 2>);
+    else
+        go(wgemm_lds_kernel<TK, TB, WK, WB, PF, 1>);
     return hipGetLastError();
 }
 
 // Kernel per shape: register-direct 64 x 16 for GEMV-like B=1 deep layers
 // (few tiles; two 16-row tiles per wave, which halves the V fragment loads
 // and doubles the U bytes each wave keeps in flight: 512@7^2 at batch 1
-// 7.1 -> 6.5 us, 1280@8^2 at batch 2 39.2 -> 34.9 us), LDS-tiled otherwise -- 128 x 128 only for K >= 512 with many
-// tiles, else 64 x 64, with two channel stages in flight once there are 128
-// tiles or more. Measured on MI355X (kernel replay, us): ResNet-50 at batch
+// 7.1 -> 6.5 us, 1280@8^2 at batch 2 39.2 -> 34.9 us), LDS-tiled otherwise
+// -- 128 x 128 only for K >= 512 with many tiles, else 64 x 64, with two
+// channel stages in flight once there are 128 tiles or more. Measured on MI355X (kernel replay, us): ResNet-50 at batch
 // 32, 128@28^2 9.7 -> 9.3 and 256@14^2 11.2 -> 10.4 with 64 x 64 (two stages)
 // instead of 128 x 128; 512@7^2 at batch 128 31.3 (128 x 128) vs 39.2; the
 // second stage in flight costs 0.1-0.5 us below 128 tiles.
