@@ -120,9 +120,17 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
 
 /* Path selection: 0 = automatic (default), 1 = force 3-pass, 2 = force the
  * fused kernel split by position row (small batches), 3 = force the fused
- * tile-block kernel (few channels, batch > 1). A forced fused path outside its
- * envelope runs 3-pass and reports an error. */
+ * tile-block kernel (few channels, batch > 1), 4 = windowed 3-pass: the batch
+ * runs in windows of whole images whose V + M fit the window budget
+ * (nova_set_window_bytes), each window's three kernels back to back -- the
+ * BP-windowed pipeline of /root/reference/tests/test_bp_tiled.hip:482-571,
+ * never chosen automatically. A forced fused path outside its envelope runs
+ * 3-pass and reports an error. */
 NOVA_API void nova_set_path(nova_handle_t h, int path);
+/* V + M bytes per window of path 4 (0 = default, 4 MiB, the reference's
+ * budget; at least one image per window). No counterpart in the reference,
+ * whose window size is computed inline (test_bp_tiled.hip:613-614). */
+NOVA_API void nova_set_window_bytes(nova_handle_t h, long long bytes);
 /* Output epilogue of every subsequent forward on the handle: d_bias_f16 is a
  * device array of K fp16 values added per output channel (NULL: none), with
  * the rounding of the reference's separate `y + bias.half()`; relu = 1 clamps
@@ -147,7 +155,7 @@ NOVA_API void nova_set_layout(nova_handle_t h, int nhwc);
  * reference (a residual there is a separate elementwise op). */
 NOVA_API void nova_set_residual(nova_handle_t h, const void* d_residual_f16);
 /* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused
- * (position rows), 3 = fused (tile blocks). */
+ * (position rows), 3 = fused (tile blocks), 4 = windowed 3-pass. */
 NOVA_API int nova_get_last_path(nova_handle_t h);
 
 /* Internal workspace bytes a forward of this shape needs on this handle. */

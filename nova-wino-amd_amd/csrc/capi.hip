@@ -39,6 +39,9 @@ void set_error(int code, const char* fmt, ...) {
 namespace {
 
 constexpr uint32_t kMagic = 0x4e4f5641u;  // "NOVA"
+// V + M bytes per window of the windowed three-pass path: the reference's
+// 4 MiB L2 budget (/root/reference/tests/test_bp_tiled.hip:613-614).
+constexpr int64_t kDefaultWindowBytes = (int64_t)4 << 20;
 
 // Kernel kinds for per-kernel timing.
 enum Kind { kKindInput = 0, kKindGemm = 1, kKindOutput = 2, kKindFused = 3, kNumKinds = 4 };
@@ -105,7 +108,8 @@ struct Handle {
     unsigned* cnt = nullptr;  // fused-kernel arrival counters, zero between launches
     size_t cnt_cap = 0;       // counters
     hipStream_t stream = nullptr;
-    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block
+    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block, 4 windowed
+    int64_t window_bytes = kDefaultWindowBytes;  // V + M per window of the windowed path
     Epilogue ep;        // bias / residual / ReLU applied by every forward
     int nhwc = 0;       // 1: x and y are NHWC (channels last)
     int last_path = 0;
@@ -243,8 +247,17 @@ bool fused_block_plan_for(const Handle* Hd, const Shape& s, FusedBlockPlan* p) {
 // Pipeline for a forward: 1 three-pass, 2 fused (position-row split), 3 fused
 // (tile block). A requested fused variant outside its envelope falls back to
 // the three-pass pipeline.
+// Images per launch of the windowed three-pass path: as many as keep V + M
+// of the window within the handle's budget (at least one image; the
+// reference windows tile ranges, this path whole images).
+int64_t window_images(const Handle* Hd, const Shape& s) {
+    const int64_t per_img = 2 * (int64_t)64 * (Hd->Cp + Hd->K) * s.nh * s.nw;
+    return std::max<int64_t>(1, Hd->window_bytes / per_img);
+}
+
 int choose_path(const Handle* Hd, const Shape& s) {
     if (Hd->path_pref == 1) return 1;
+    if (Hd->path_pref == 4) return 4;
     if (Hd->path_pref == 2) {
         if (Hd->nhwc) return 1;  // the position-row kernel reads and writes NCHW only
         FusedPlan p;
@@ -318,7 +331,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         return;
     }
     if (s_all.B == 0) return;
-    const int64_t chunk = batch_chunk(Hd, s_all);
+    int64_t chunk = batch_chunk(Hd, s_all);
     if (chunk < 1) {
         set_error(kErrInvalidArgument, "%s: a single image of this shape exceeds 1 GB buffers", fn);
         return;
@@ -326,8 +339,9 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     int path = choose_path(Hd, s_all);
     // the channels-last tile-block kernel stages x with 16-byte loads
     if (path == 3 && Hd->nhwc && !aligned16(x)) path = 1;
-    const bool fused = path != 1;
-    if (path == 1 && Hd->path_pref >= 2) {
+    if (path == 4) chunk = std::min(chunk, window_images(Hd, s_all));
+    const bool fused = path == 2 || path == 3;
+    if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3)) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
     Hd->last_path = path;
@@ -636,11 +650,21 @@ void nova_set_stream(nova_handle_t h, void* stream) {
 void nova_set_path(nova_handle_t h, int path) {
     Handle* H = as_handle(h, "nova_set_path");
     if (!H) return;
-    if (path < 0 || path > 3) {
-        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2 or 3");
+    if (path < 0 || path > 4) {
+        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2, 3 or 4");
         return;
     }
     H->path_pref = path;
+}
+
+void nova_set_window_bytes(nova_handle_t h, long long bytes) {
+    Handle* H = as_handle(h, "nova_set_window_bytes");
+    if (!H) return;
+    if (bytes < 0) {
+        set_error(kErrInvalidArgument, "nova_set_window_bytes: bytes must be >= 0");
+        return;
+    }
+    H->window_bytes = bytes == 0 ? kDefaultWindowBytes : (int64_t)bytes;
 }
 
 void nova_set_epilogue(nova_handle_t h, const void* d_bias_f16, int relu) {
@@ -680,8 +704,10 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     if (!Hd) return -1;
     Shape s;
     if (!make_shape(Hd, batch, H, W, pad, &s, "nova_workspace_bytes")) return -1;
-    if (Hd->ready && choose_path(Hd, s) != 1) return 0;
-    const int64_t chunk = std::max<int64_t>(1, batch_chunk(Hd, s));
+    const int path = Hd->ready ? choose_path(Hd, s) : 1;
+    if (path == 2 || path == 3) return 0;
+    int64_t chunk = std::max<int64_t>(1, batch_chunk(Hd, s));
+    if (path == 4) chunk = std::min(chunk, window_images(Hd, s));
     const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;
     return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * BPc * 2);
 }

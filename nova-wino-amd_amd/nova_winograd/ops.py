@@ -53,6 +53,7 @@ _SIGNATURES = {
     "nova_get_last_error_message": (ctypes.c_char_p, []),
     "nova_set_stream": (None, [_vp, _vp]),
     "nova_set_path": (None, [_vp, _i]),
+    "nova_set_window_bytes": (None, [_vp, ctypes.c_longlong]),
     "nova_set_epilogue": (None, [_vp, _vp, _i]),
     "nova_set_weights_f16": (None, [_vp, _vp, _i, _i]),
     "nova_set_residual": (None, [_vp, _vp]),
