@@ -146,11 +146,11 @@ static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 // (two MFMA k-steps): every stage is copied global -> registers -> LDS with
 // 16-byte loads (one 128-byte line per row when Cp >= 64), double buffered so
 // the next stage's loads are in flight while the current one is multiplied.
-// LDS rows are padded to 72 halves (144 B = 36 banks), which makes the
-// 16-byte fragment reads of 8 consecutive lanes hit 8 disjoint bank groups.
+// LDS rows are 128 bytes with an XOR swizzle of their 16-byte chunks (see
+// the kernel), conflict-free for both the staging writes and the fragment
+// reads.
 // ---------------------------------------------------------------------------
 constexpr int kStageC = 64;
-constexpr int kPitch = 72;
 
 template <int TK, int TB, int WK, int WB, int PF, int SM>
 __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restrict__ U,
@@ -164,8 +164,14 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
     constexpr int kChunksV = TB * kStageC / 8;
     constexpr int kPerThreadU = (kChunksU + 255) / 256;
     constexpr int kPerThreadV = (kChunksV + 255) / 256;
-    __shared__ __align__(16) _Float16 sU[2][TK * kPitch];
-    __shared__ __align__(16) _Float16 sV[2][TB * kPitch];
+    // Double-buffered stages, U then V: rows of kStageC channels (128 bytes),
+    // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7). The XOR
+    // swizzle keeps both access patterns conflict-free on the 64 banks: the
+    // staging writes (8 lanes per row, two rows per 16 lanes) and the
+    // fragment reads (16 lanes on 16 consecutive rows, one chunk each).
+    __shared__ __align__(16) _Float16 smem[2 * (TK + TB) * kStageC];
+    auto sU = [&](int buf) { return smem + buf * TK * kStageC; };
+    auto sV = [&](int buf) { return smem + 2 * TK * kStageC + buf * TB * kStageC; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -196,7 +202,7 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         const int row = ch >> 3, cg = ch & 7;
         const bool ok = ch < kChunksU && k0 + row < K;
         uoff[j] = ok ? 2 * ((k0 + row) * Cp + cg * 8) : kOob;
-        ulds[j] = ch < kChunksU ? row * kPitch + cg * 8 : -1;
+        ulds[j] = ch < kChunksU ? row * kStageC + (cg ^ ((row >> 1) & 7)) * 8 : -1;
     }
 #pragma unroll
     for (int j = 0; j < kPerThreadV; j++) {
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         const int row = ch >> 3, cg = ch & 7;
         const bool ok = ch < kChunksV && n0 + row < BP;
         voff[j] = ok ? 2 * ((n0 + row) * Cp + cg * 8) : kOob;
-        vlds[j] = ch < kChunksV ? row * kPitch + cg * 8 : -1;
+        vlds[j] = ch < kChunksV ? row * kStageC + (cg ^ ((row >> 1) & 7)) * 8 : -1;
     }
     const int nstages = (Cp + kStageC - 1) / kStageC;
     // PF stages in flight in registers: slot st % PF holds stage st from its
@@ -230,10 +236,10 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
     auto lstore = [&](int buf, const h8 (&u)[kPerThreadU], const h8 (&v)[kPerThreadV]) {
 #pragma unroll
         for (int j = 0; j < kPerThreadU; j++)
-            if (ulds[j] >= 0) *reinterpret_cast<h8*>(&sU[buf][ulds[j]]) = u[j];
+            if (ulds[j] >= 0) *reinterpret_cast<h8*>(sU(buf) + ulds[j]) = u[j];
 #pragma unroll
         for (int j = 0; j < kPerThreadV; j++)
-            if (vlds[j] >= 0) *reinterpret_cast<h8*>(&sV[buf][vlds[j]]) = v[j];
+            if (vlds[j] >= 0) *reinterpret_cast<h8*>(sV(buf) + vlds[j]) = v[j];
     };
 
     f4 acc[MT][NT];
@@ -254,17 +260,21 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
             if (st >= nstages) break;
             const int buf = st & 1;
             if (st + PF < nstages) gload(st + PF, ru[j], rv[j]);
-            const _Float16* su = sU[buf] + (wk * MT * 16 + r16) * kPitch + 8 * g;
-            const _Float16* sv = sV[buf] + (wb * NT * 16 + r16) * kPitch + 8 * g;
+            // lane (row r16 of each 16-row tile, chunk 4*kk + g); every tile
+            // starts at a multiple of 16 rows, so the swizzle depends on r16
+            const int c0 = g ^ ((r16 >> 1) & 7);
+            const _Float16* su = sU(buf) + (wk * MT * 16 + r16) * kStageC;
+            const _Float16* sv = sV(buf) + (wb * NT * 16 + r16) * kStageC;
 #pragma unroll
             for (int kk = 0; kk < kStageC / 32; kk++) {
+                const int co = (c0 ^ (4 * kk)) * 8;
                 h8 a[MT], b[NT];
 #pragma unroll
                 for (int mi = 0; mi < MT; mi++)
-                    a[mi] = *reinterpret_cast<const h8*>(su + mi * 16 * kPitch + kk * 32);
+                    a[mi] = *reinterpret_cast<const h8*>(su + mi * 16 * kStageC + co);
 #pragma unroll
                 for (int ni = 0; ni < NT; ni++)
-                    b[ni] = *reinterpret_cast<const h8*>(sv + ni * 16 * kPitch + kk * 32);
+                    b[ni] = *reinterpret_cast<const h8*>(sv + ni * 16 * kStageC + co);
 #pragma unroll
                 for (int mi = 0; mi < MT; mi++)
 #pragma unroll
@@ -284,8 +294,8 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         // L2 then holds whole dirty lines instead of 32-byte pieces of 16.
         if ((K & 7) == 0) {
             constexpr int kMP = TK + 8;  // halves per staged row
-            static_assert(TB * kMP <= 2 * TK * kPitch, "M tile fits in sU");
-            _Float16* sm = &sU[0][0];
+            static_assert(TB * kMP <= 2 * (TK + TB) * kStageC, "M tile fits in the stages");
+            _Float16* sm = smem;
 #pragma unroll
             for (int mi = 0; mi < MT; mi++)
 #pragma unroll
