@@ -142,7 +142,7 @@ static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 
 // ---------------------------------------------------------------------------
 // LDS-tiled variant for larger shapes. Workgroup tile = TK output channels x
-// TB tiles (bp) of one position, 4 waves (WK x WB), channels in stages of 64
+// TB tiles (bp) of one position, WK x WB waves, channels in stages of 64
 // (two MFMA k-steps): every stage is copied global -> registers -> LDS with
 // 16-byte loads (one 128-byte line per row when Cp >= 64), double buffered so
 // the next stage's loads are in flight while the current one is multiplied.
@@ -153,17 +153,17 @@ static hipError_t launch_cfg(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 constexpr int kStageC = 64;
 
 template <int TK, int TB, int WK, int WB, int PF, int SM>
-__global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restrict__ U,
+__global__ __launch_bounds__(64 * WK * WB) void wgemm_lds_kernel(const _Float16* __restrict__ U,
                                                         const _Float16* __restrict__ V,
                                                         _Float16* __restrict__ M, int K, int Cp,
                                                         int BP) {
-    static_assert(WK * WB == 4, "4 waves");
+    constexpr int kThreads = 64 * WK * WB;
     constexpr int MT = TK / WK / 16;  // 16x16 tiles per wave along k
     constexpr int NT = TB / WB / 16;  // along bp
     constexpr int kChunksU = TK * kStageC / 8;  // 16-byte chunks per stage
     constexpr int kChunksV = TB * kStageC / 8;
-    constexpr int kPerThreadU = (kChunksU + 255) / 256;
-    constexpr int kPerThreadV = (kChunksV + 255) / 256;
+    constexpr int kPerThreadU = (kChunksU + kThreads - 1) / kThreads;
+    constexpr int kPerThreadV = (kChunksV + kThreads - 1) / kThreads;
     // Double-buffered stages, U then V: rows of kStageC channels (128 bytes),
     // 16-byte chunk c of row r stored at chunk c ^ ((r >> 1) & 7). The XOR
     // swizzle keeps both access patterns conflict-free on the 64 banks: the
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
     int uoff[kPerThreadU], ulds[kPerThreadU], voff[kPerThreadV], vlds[kPerThreadV];
 #pragma unroll
     for (int j = 0; j < kPerThreadU; j++) {
-        const int ch = tid + j * 256;
+        const int ch = tid + j * kThreads;
         const int row = ch >> 3, cg = ch & 7;
         const bool ok = ch < kChunksU && k0 + row < K;
         uoff[j] = ok ? 2 * ((k0 + row) * Cp + cg * 8) : kOob;
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
     }
 #pragma unroll
     for (int j = 0; j < kPerThreadV; j++) {
-        const int ch = tid + j * 256;
+        const int ch = tid + j * kThreads;
         const int row = ch >> 3, cg = ch & 7;
         const bool ok = ch < kChunksV && n0 + row < BP;
         voff[j] = ok ? 2 * ((n0 + row) * Cp + cg * 8) : kOob;
@@ -220,14 +220,14 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
         const int c = st * kStageC;
 #pragma unroll
         for (int j = 0; j < kPerThreadU; j++) {
-            const int cg = (tid + j * 256) & 7;
+            const int cg = (tid + j * kThreads) & 7;
             const bool cok = c + cg * 8 < Cp;
             u[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
                                               urs, cok ? uoff[j] : kOob, au + 2 * c, 0));
         }
 #pragma unroll
         for (int j = 0; j < kPerThreadV; j++) {
-            const int cg = (tid + j * 256) & 7;
+            const int cg = (tid + j * kThreads) & 7;
             const bool cok = c + cg * 8 < Cp;
             v[j] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
                                               vrs, cok ? voff[j] : kOob, bu + 2 * c, 0));
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(256) void wgemm_lds_kernel(const _Float16* __restri
             typedef unsigned u4 __attribute__((ext_vector_type(4)));
             constexpr int kCh = TK / 8;  // 16-byte chunks per row
 #pragma unroll
-            for (int e = tid; e < TB * kCh; e += 256) {
+            for (int e = tid; e < TB * kCh; e += kThreads) {
                 const int row = e / kCh, ch = e % kCh;
                 const int bp = n0 + row, k = k0 + 8 * ch;
                 const u4 v = *reinterpret_cast<const u4*>(sm + row * kMP + 8 * ch);
@@ -361,7 +361,7 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
                              int BP, hipStream_t s) {
     const unsigned grid = 64u * (unsigned)((BP + TB - 1) / TB) * (unsigned)((K + TK - 1) / TK);
     auto go = [&](auto kernel) {
-        launch(kernel, dim3(grid), dim3(256), s, reinterpret_cast<const _Float16*>(U),
+        launch(kernel, dim3(grid), dim3(64 * WK * WB), s, reinterpret_cast<const _Float16*>(U),
                reinterpret_cast<const _Float16*>(V), reinterpret_cast<_Float16*>(M), K, Cp, BP);
     };
     if (m_epilogue(K, BP) == 2)
@@ -376,14 +376,19 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 // and doubles the U bytes each wave keeps in flight: 512@7^2 at batch 1
 // 7.1 -> 6.5 us, 1280@8^2 at batch 2 39.2 -> 34.9 us), LDS-tiled otherwise
 // -- 128 x 128 only for K >= 512 with many tiles, else 64 x 64, with two
-// channel stages in flight once there are 128 tiles or more. Measured on MI355X (kernel replay, us): ResNet-50 at batch
+// channel stages in flight once there are 128 tiles or more. 8 waves per
+// workgroup except for 64 x 64 tiles at K > 256 below 128 tiles (whole
+// forwards, us, 4 -> 8 waves: 512@7^2 batch 32 27.2 -> 26.3 and batch 64
+// 34.7 -> 32.5; 128@28^2 batch 128 66.2 -> 63.1; 64@56^2 batch 1 10.6 ->
+// 10.4; but 1280@32^2 batch 1 52.5 -> 55.9). Measured on MI355X (kernel replay, us): ResNet-50 at batch
 // 32, 128@28^2 9.7 -> 9.3 and 256@14^2 11.2 -> 10.4 with 64 x 64 (two stages)
 // instead of 128 x 128; 512@7^2 at batch 128 31.3 (128 x 128) vs 39.2; the
 // second stage in flight costs 0.1-0.5 us below 128 tiles.
 static int wgemm_cfg(int K, int BP) {
     if (BP <= 16) return 0;
     if (K >= 512 && BP >= 128) return 2;
-    return BP >= 128 ? 3 : 1;
+    if (BP >= 128) return 3;
+    return K <= 256 ? 4 : 1;
 }
 
 int wgemm_v_reads(int K, int BP) {
@@ -394,8 +399,9 @@ int wgemm_v_reads(int K, int BP) {
 const char* wgemm_name(int K, int Cp, int BP) {
     (void)Cp;
     static const char* names[] = {"wgemm_kernel<2, 1, 2, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2, 1>",
-                                  "wgemm_lds_kernel<128, 128, 2, 2, 1>",
-                                  "wgemm_lds_kernel<64, 64, 2, 2, 2>"};
+                                  "wgemm_lds_kernel<128, 128, 2, 4, 1>",
+                                  "wgemm_lds_kernel<64, 64, 2, 4, 2>",
+                                  "wgemm_lds_kernel<64, 64, 2, 4, 1>"};
     return names[wgemm_cfg(K, BP)];
 }
 
@@ -404,8 +410,9 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
     switch (wgemm_cfg(K, BP)) {
         case 0: return launch_cfg<2, 1, 2, 1, 4>(U, V, M, K, Cp, BP, s);
         case 1: return launch_lds<64, 64, 2, 2, 1>(U, V, M, K, Cp, BP, s);
-        case 2: return launch_lds<128, 128, 2, 2, 1>(U, V, M, K, Cp, BP, s);
-        default: return launch_lds<64, 64, 2, 2, 2>(U, V, M, K, Cp, BP, s);
+        case 2: return launch_lds<128, 128, 2, 4, 1>(U, V, M, K, Cp, BP, s);
+        case 3: return launch_lds<64, 64, 2, 4, 2>(U, V, M, K, Cp, BP, s);
+        default: return launch_lds<64, 64, 2, 4, 1>(U, V, M, K, Cp, BP, s);
     }
 }
 

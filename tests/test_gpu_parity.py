@@ -124,14 +124,16 @@ def test_output_transform_bitexact(oracle, B, K, Ho, Wo):
 
 # Then: larger BP with K, Cp <= 128 (several bp tiles per position on the
 # 64 x 64 kernel with two stages in flight), partial 32-channel steps, K not a
-# multiple of 4; last, K >= 512 with BP >= 128 (the 128 x 128 kernel), with a
-# partial k tile and a partial bp tile.
+# multiple of 4; then K >= 512 with BP >= 128 (the 128 x 128 kernel), with a
+# partial k tile and a partial bp tile; last, K > 256 below 128 tiles (the
+# four-wave 64 x 64 kernel).
 GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256, 28),
               (1, 256, 256, 14), (1, 16, 40, 9), (8, 128, 128, 28), (2, 136, 200, 30),
               (4, 72, 132, 40),
               (16, 64, 64, 56), (12, 128, 128, 28), (12, 40, 24, 30), (12, 104, 100, 28),
               (12, 96, 98, 28),
-              (32, 40, 520, 7), (33, 24, 516, 7)]
+              (32, 40, 520, 7), (33, 24, 516, 7),
+              (2, 64, 320, 14), (3, 48, 264, 20)]
 
 
 @pytest.mark.parametrize("B,C,K,H", GEMM_CASES)
