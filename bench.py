@@ -210,7 +210,10 @@ def traffic_from(fetch_dir, write_dir, out_path):
         for name in NOVA_KERNELS:
             kern = [r for r in rows if any(k in r[0] for k in _name_keys(name))]
             if kern:
-                per[name] = (sum(r[2] for r in kern) / len(kern) * 1024.0 * factor,
+                # mean over dispatches (a row can hold several layers that
+                # share a kernel and a grid size)
+                per[name] = (sum(r[2] * r[3] for r in kern) / sum(r[3] for r in kern)
+                             * 1024.0 * factor,
                              [(r[1], round(r[2], 1)) for r in kern])
         return per, factor, copy_kib
 
