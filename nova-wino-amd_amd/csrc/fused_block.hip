@@ -284,12 +284,23 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 },
                 [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
         }
+        // the first k-step's U fragments are requested before the barrier, so
+        // their L2 latency overlaps the wait for the slowest wave's transform
+        h4 ua0[8][4];
+        load_u(a, urs, wave, k0 / 16, (c0 >> 4), lane, ua0);
         __syncthreads();
         // -- products: this wave's position row, two 16-channel k-steps --
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             h4 ua[8][4];
-            load_u(a, urs, wave, k0 / 16, (c0 >> 4) + ks, lane, ua);
+            if (ks == 0) {
+#pragma unroll
+                for (int s = 0; s < 8; s++)
+#pragma unroll
+                    for (int kb = 0; kb < 4; kb++) ua[s][kb] = ua0[s][kb];
+            } else {
+                load_u(a, urs, wave, k0 / 16, (c0 >> 4) + ks, lane, ua);
+            }
             h4 vf[8];
 #pragma unroll
             for (int s = 0; s < 8; s++)
