@@ -326,11 +326,11 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         set_error(kErrNotInitialized, "%s: call nova_set_weights() before forward", fn);
         return;
     }
+    if (s_all.B == 0) return;  // nothing to read or write (an empty tensor's pointer may be null)
     if (x == nullptr || y == nullptr) {
         set_error(kErrInvalidArgument, "%s: null input or output pointer", fn);
         return;
     }
-    if (s_all.B == 0) return;
     int64_t chunk = batch_chunk(Hd, s_all);
     if (chunk < 1) {
         set_error(kErrInvalidArgument, "%s: a single image of this shape exceeds 1 GB buffers", fn);
