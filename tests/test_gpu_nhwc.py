@@ -112,6 +112,22 @@ def test_nhwc_fused_block_equals_nchw(B, C, K, H, pad):
         assert torch.equal(ya, y)
 
 
+@pytest.mark.parametrize("B,C,K,H,W,pad", [(6, 64, 48, 30, 44, 1), (5, 32, 64, 17, 58, 0),
+                                             (3, 24, 40, 50, 14, 2)])
+def test_nhwc_non_square(B, C, K, H, W, pad):
+    """Non-square images, both paths: NHWC equals NCHW bit for bit."""
+    print(f"[nhwc] non-square B={B} C={C} K={K} H={H} W={W} pad={pad}", flush=True)
+    torch.manual_seed(17)
+    x = torch.randn(B, C, H, W, device=DEV).half()
+    w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
+    xc = x.contiguous(memory_format=CL)
+    for path in (1, 3):
+        y_ref, took_ref = _run(x, w, pad, False, path=path)
+        y, took = _run(xc, w, pad, True, path=path)
+        assert took == took_ref, (path, took, took_ref)
+        assert torch.equal(y, y_ref), path
+
+
 def test_nhwc_unaligned_input():
     torch.manual_seed(13)
     B, C, K, H = 8, 64, 64, 56
