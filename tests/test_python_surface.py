@@ -103,3 +103,39 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_bench_kernel_stats_summary(tmp_path):
+    """bench.py's kernel-trace summary writer: per-family agreement of the
+    bench line's event times with a rocprofv3 trace (synthetic CSVs here)."""
+    import importlib.util
+    import json
+    import os
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    trace = tmp_path / "trace"
+    trace.mkdir()
+    (trace / "run_kernel_stats.csv").write_text(
+        '"Name","Calls","TotalDurationNs","AverageNs","Percentage","MinNs","MaxNs","StdDev"\n'
+        '"_ZN4nova16wgemm_lds_kernelILi64E",4,40000,10000.0,60.0,9000,11000,1.0\n'
+        '"_ZN4nova22input_transform_kernelILi2E",4,20000,5000.0,40.0,4000,6000,1.0\n')
+    rows = ["Kernel_Name,Grid_Size_X,Grid_Size_Y,Grid_Size_Z,Start_Timestamp,End_Timestamp"]
+    for i in range(4):
+        rows.append(f"_ZN4nova16wgemm_lds_kernelILi64E,1024,1,1,{1000 * i},{1000 * i + 10000}")
+        rows.append(f"_ZN4nova15input_lp_kernelILb0E,256,1,1,{1000 * i},{1000 * i + 5000}")
+    (trace / "run_kernel_trace.csv").write_text("\n".join(rows) + "\n")
+    line = {"value": 1.0, "ms_per_step": 0.1,
+            "roofline": {"kernel": "wgemm", "avg_launch_us": 11.0, "achieved": 1.0, "frac": 0.1,
+                         "peak": 8000.0},
+            "kernel_families": {"wgemm": {"avg_launch_us": 11.0},
+                                "input_transform_kernel": {"avg_launch_us": 5.5}}}
+    bl = tmp_path / "line.json"
+    bl.write_text("log line\n" + json.dumps(line) + "\n")
+    out = tmp_path / "summary.md"
+    bench.kernel_stats_from(str(trace), str(bl), str(out))
+    text = out.read_text()
+    assert "| wgemm | 11.000 | 10.000 | 4 | 1.100 |" in text
+    assert "| input_transform_kernel | 5.500 | 5.000 | 4 | 1.100 |" in text
