@@ -471,6 +471,29 @@ def extra_measurements(runs, lib, torch, nn, nw, reps):
         log(f"{name:18s} B={B:<3d} {rec['path']:11s} nova {tn*1e3:9.2f} us  miopen "
             f"{tm*1e3:9.2f} us")
         del x, mod, mio
+    # channels-last activations (an extension): the headline layers at B=32
+    # with NHWC input and output, NOVA (NHWC kernels) vs MIOpen on the same
+    # channels-last tensor
+    out["nhwc"] = []
+    for r in runs:
+        if r["B"] == 1:
+            continue
+        xc = r["x"].contiguous(memory_format=torch.channels_last)
+        mio = r["mio"].to(memory_format=torch.channels_last)
+        with torch.no_grad():
+            r["mod"](xc)
+            mio(xc)
+            tn = time_region(lambda: r["mod"](xc), reps, torch)
+            tm = time_region(lambda: mio(xc), reps, torch)
+        rec = {"layer": r["name"], "B": r["B"],
+               "path": path_names.get(lib.nova_get_last_path(r["mod"]._handle.h), "?"),
+               "nova_ms": round(tn, 5), "miopen_ms": round(tm, 5),
+               "speedup_vs_miopen": round(tm / tn, 3)}
+        out["nhwc"].append(rec)
+        log(f"{r['name']:8s} B={r['B']:<3d} NHWC {rec['path']:11s} nova {tn*1e3:8.2f} us  "
+            f"miopen {tm*1e3:8.2f} us")
+        r["mio"].to(memory_format=torch.contiguous_format)
+        del xc
     # full ResNet-50, eager, MIOpen fp16 vs after surgery
     import copy
     sys.path.insert(0, os.path.join(ROOT, "tests"))
