@@ -179,14 +179,15 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
         __syncthreads();  // the previous chunk is done with the staging area and V
         // -- stage the chunk's input rows --
         if constexpr (kNhwc) {
-            // units (row r, pixel pc, 8-channel group g), 8 loads in flight per thread
+            // units (row r, pixel pc, 8-channel group g), 4 loads in flight per
+            // thread (8 spill registers beside the accumulators: 5 % slower)
             const int nunits = rows_st * a.cols * 4;
             _Float16* xh = reinterpret_cast<_Float16*>(xs);
-            for (int e0 = 0; e0 < nunits; e0 += 8 * kBT) {
-                u4 v[8];
-                int dst[8];
+            for (int e0 = 0; e0 < nunits; e0 += 4 * kBT) {
+                u4 v[4];
+                int dst[4];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
+                for (int u = 0; u < 4; u++) {
                     const int e = e0 + tid + u * kBT;
                     const int g = e & 3, rp = e >> 2;
                     const int r = rp / a.cols, pc = rp - (rp / a.cols) * a.cols;
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                     dst[u] = live ? (r * a.cols + pc) * kNhwcPix + 8 * g : -1;
                 }
 #pragma unroll
-                for (int u = 0; u < 8; u++)
+                for (int u = 0; u < 4; u++)
                     if (dst[u] >= 0) {  // 8-byte aligned: two 8-byte writes
                         *reinterpret_cast<u2*>(xh + dst[u]) = u2{v[u][0], v[u][1]};
                         *reinterpret_cast<u2*>(xh + dst[u] + 4) = u2{v[u][2], v[u][3]};
