@@ -163,10 +163,11 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 
     // ---- staging spans: (channel c, staged row r), kSpr per thread per round ----
     // Each span is NJ 16-byte loads at immediate offsets, all of a round in
-    // flight at once (two spans per round while their registers fit beside
-    // the accumulators, else one); rows outside the image and channels past C
-    // get an out-of-range offset, so zeros are staged for them.
-    constexpr int kSpr = NJ <= 5 ? 2 : 1;
+    // flight at once (one span per thread and round: two would need spill
+    // registers beside the accumulators); rows outside the image and
+    // channels past C get an out-of-range offset, so zeros are staged for
+    // them.
+    constexpr int kSpr = 1;
     const int nspans = kBCC * rows_st;
 
     f4 acc[8][4];
@@ -285,22 +286,32 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 },
                 [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
         }
-        // the first k-step's U fragments are requested before the barrier, so
-        // their L2 latency overlaps the wait for the slowest wave's transform
-        h4 ua0[8][4];
-        load_u(a, urs, wave, k0 / 16, (c0 >> 4), lane, ua0);
+        // half of the first k-step's U fragments (positions 0..3 of this
+        // wave's row) are requested before the barrier, so their L2 latency
+        // overlaps the wait for the slowest wave's transform (all of them
+        // would not fit beside the accumulators without spilling)
+        h4 ua0[4][4];
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const int kt = k0 / 16 + kb;
+                const int soff =
+                    kt < a.nkt ? (((8 * wave + s) * a.nkt + kt) * a.nks + (c0 >> 4)) * 512 : kBOob;
+                ua0[s][kb] = __builtin_bit_cast(
+                    h4, __builtin_amdgcn_raw_buffer_load_b64(urs, lane * 8, soff, 0));
+            }
         __syncthreads();
         // -- products: this wave's position row, two 16-channel k-steps --
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             h4 ua[8][4];
-            if (ks == 0) {
+            load_u(a, urs, wave, k0 / 16, (c0 >> 4) + ks, lane, ua);
+            if (ks == 0) {  // positions 0..3 already loaded
 #pragma unroll
-                for (int s = 0; s < 8; s++)
+                for (int s = 0; s < 4; s++)
 #pragma unroll
                     for (int kb = 0; kb < 4; kb++) ua[s][kb] = ua0[s][kb];
-            } else {
-                load_u(a, urs, wave, k0 / 16, (c0 >> 4) + ks, lane, ua);
             }
             h4 vf[8];
 #pragma unroll
