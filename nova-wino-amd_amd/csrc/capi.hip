@@ -113,6 +113,7 @@ struct Handle {
     Epilogue ep;        // bias / residual / ReLU applied by every forward
     int nhwc = 0;       // 1: x and y are NHWC (channels last)
     int last_path = 0;
+    int cus = 256;  // compute units of the device the weights were set on
     bool ready = false;
     Profiler prof;
 };
@@ -268,16 +269,20 @@ int choose_path(const Handle* Hd, const Shape& s) {
         return fused_block_plan_for(Hd, s, &p) ? 3 : 1;
     }
     // Automatic choice, from MI355X measurements: the tile-block fused kernel
-    // wins for layers with at most 64 input and output channels once there
-    // are enough 16-tile runs to occupy the chip, and while each CU runs at
-    // most two of its workgroups one after the other (ResNet-50 conv2_x,
-    // NCHW: B=32 31.7 us vs 39.3 us three-pass, B=64 60.6 vs 65.4, but B=128
-    // 115 vs 112 and B=16 29.8 vs 25.4; NHWC: B=32 33.2 vs 36.2); everything
+    // for layers with at most 64 input and output channels, when its
+    // workgroups (one per CU at a time, ~28 us each at conv2_x) fill their
+    // last wave over the CUs to at least 80 %: its time steps by whole waves
+    // while the three-pass time grows with the batch. ResNet-50 conv2_x
+    // forwards, us, three-pass vs fused: B=16 27.0 vs 29.5 (grid 112), B=32
+    // 36.1 vs 30.0 (224: 88 % fill), B=40 42.4 vs 50.0 (280: 55 %), B=48
+    // 48.8 vs 56.4 (66 %), B=64 59.6 vs 57.7 (88 %), B=80 71.3 vs 77.8
+    // (73 %), B=128 120.7 vs 111.3, B=256 260.6 vs 194.8 (88 %); everything
     // else runs three-pass.
     FusedBlockPlan bp;
-    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp) && bp.grid >= 128 &&
-        bp.grid <= 2 * 256)
-        return 3;
+    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp) && bp.grid >= 128) {
+        const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
+        if (bp.grid * 5 >= waves * Hd->cus * 4) return 3;
+    }
     return 1;
 }
 
@@ -502,6 +507,11 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
     H->K = K;
     H->C = C;
     H->Cp = Cp;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0)
+        H->cus = cus;
     H->ready = hip_ok(launch_filter_transform_gemm(d_weight, w_f16, H->U, K, C, Cp, H->stream),
                       "filter transform") &&
                hip_ok(launch_u_frag(H->U, H->Uf, K, Cp, H->stream), "filter fragment order");

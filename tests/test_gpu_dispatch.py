@@ -57,9 +57,10 @@ def _forward(lib, path, x, w, pad):
 
 # (B, C, K, H, expected automatic path)
 AUTO_CASES = [
-    (32, 64, 64, 56, 3),   # ResNet-50 conv2_x, B=32: fused tile-block kernel
-    (64, 64, 64, 56, 3),   # two workgroups per CU: still fused
-    (128, 64, 64, 56, 1),  # four per CU: three-pass is faster
+    (32, 64, 64, 56, 3),   # ResNet-50 conv2_x, B=32: fused tile-block kernel (88 % fill)
+    (48, 64, 64, 56, 1),   # two waves of workgroups, the second 32 % full: three-pass
+    (64, 64, 64, 56, 3),   # two waves, 88 % fill: fused
+    (128, 64, 64, 56, 3),  # four waves, 88 % fill: fused
     (32, 128, 128, 28, 1),  # conv3_x: three-pass
     (1, 64, 64, 56, 1),    # B=1: three-pass
 ]
