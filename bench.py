@@ -265,11 +265,11 @@ def kernel_stats_from(trace_dir, bench_json, out_path):
         "Commands (from the repository root, on one MI355X):",
         "",
         "```",
-        "python3 -u bench.py --no-extra > gpurun_out/bench_line.json",
+        "python3 -u bench.py --details out/bench_details.json > out/bench_line.json",
         "cd /tmp && export TMPDIR=/tmp && cd - && rocprofv3 --kernel-trace --stats "
-        "--output-format csv -d gpurun_out/prof_bench -o bench -- python3 -u bench.py "
+        "--output-format csv -d out/prof_bench -o bench -- python3 -u bench.py "
         "--no-extra --no-cpu",
-        "python3 bench.py --kernel-stats-from gpurun_out/prof_bench gpurun_out/bench_line.json"
+        "python3 bench.py --kernel-stats-from out/prof_bench out/bench_line.json"
         "   # -> this file",
         "```",
         "",
@@ -329,11 +329,11 @@ def write_traffic_summary(data, path):
         "",
         "```",
         "cd /tmp && export TMPDIR=/tmp && cd -",
-        "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o pmc -- "
+        "timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE -d out/pmc_fetch -o pmc -- "
         "python3 -u bench.py --pmc-mode",
-        "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc -- "
+        "timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE -d out/pmc_write -o pmc -- "
         "python3 -u bench.py --pmc-mode",
-        "python3 bench.py --traffic-from gpurun_out/pmc_fetch gpurun_out/pmc_write   "
+        "python3 bench.py --traffic-from out/pmc_fetch out/pmc_write   "
         "# -> profiles/traffic.json + this file",
         "```",
         "",
@@ -584,8 +584,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the NOVA conv shards by batch or output channel with no exchange; "
-              "see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the NOVA conv would shard by batch or by output channel, with no "
+              "exchange during a layer). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
