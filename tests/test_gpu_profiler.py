@@ -70,3 +70,40 @@ def test_profile_counts_and_intervals(path, B, C, K, H):
         check()
     finally:
         lib.nova_destroy(h)
+
+
+@pytest.mark.parametrize("path,B,C,K,H", [(1, 2, 64, 64, 28), (3, 32, 64, 64, 56)])
+def test_profile_replay(path, B, C, K, H):
+    """nova_profile_replay re-launches the last forward's kernels (they are
+    idempotent: the output is unchanged), returns a positive mean time for
+    every kind the forward launched and an error for the others."""
+    from nova_winograd.ops import check, get_lib
+
+    print(f"[profiler] replay path={path} B={B}", flush=True)
+    lib = get_lib()
+    torch.manual_seed(4)
+    x = torch.randn(B, C, H, H, device=DEV).half()
+    w = (torch.randn(K, C, 3, 3, device=DEV) * 0.05).float()
+    y = torch.empty(B, K, H, H, dtype=torch.float16, device=DEV)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_path(h, path)
+        lib.nova_set_weights(h, w.data_ptr(), K, C)
+        lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, H, 1)
+        check()
+        torch.cuda.synchronize()
+        y0 = y.clone()
+        kinds = [0, 1, 2] if path == 1 else [3]
+        for k in range(4):
+            ms = lib.nova_profile_replay(h, k, 5)
+            if k in kinds:
+                assert ms > 0.0, k
+                assert lib.nova_get_last_error() == 0
+            else:
+                assert ms < 0.0
+                assert lib.nova_get_last_error() != 0
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0)
+        assert lib.nova_get_U_gemm(h)
+    finally:
+        lib.nova_destroy(h)
