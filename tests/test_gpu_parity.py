@@ -278,3 +278,53 @@ def test_forward_follows_stream(oracle):
     finally:
         lib.nova_destroy(h)
     assert oracle.rel_l2(y.cpu().numpy(), yo) < 5e-3
+
+
+def test_concurrent_handles_on_two_streams():
+    """Two handles on two streams (default priority) run different layers and
+    paths concurrently, each forward repeated; every result equals the same
+    forward run alone on the default stream, bit for bit."""
+    lib = _lib()
+    cases = [(32, 64, 64, 56, 0), (8, 128, 96, 28, 1)]  # fused tile-block, three-pass
+    data, ref = [], []
+    torch.manual_seed(61)
+    for B, C, K, H, path in cases:
+        x = torch.randn(B, C, H, H, device=DEV).half()
+        w = (torch.randn(K, C, 3, 3, device=DEV) * 0.05).float()
+        data.append((x, w))
+        y = torch.empty(B, K, H, H, dtype=torch.float16, device=DEV)
+        h = lib.nova_create()
+        try:
+            lib.nova_set_path(h, path)
+            lib.nova_set_weights(h, w.data_ptr(), K, C)
+            lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, H, 1)
+            _check()
+            torch.cuda.synchronize()
+        finally:
+            lib.nova_destroy(h)
+        ref.append(y)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    handles = [lib.nova_create(), lib.nova_create()]
+    outs = [[], []]
+    try:
+        for i, ((B, C, K, H, path), (x, w)) in enumerate(zip(cases, data)):
+            lib.nova_set_stream(handles[i], ctypes.c_void_p(streams[i].cuda_stream))
+            lib.nova_set_path(handles[i], path)
+            streams[i].wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(streams[i]):
+                lib.nova_set_weights(handles[i], w.data_ptr(), K, C)
+        for rep in range(4):
+            for i, ((B, C, K, H, path), (x, w)) in enumerate(zip(cases, data)):
+                with torch.cuda.stream(streams[i]):
+                    y = torch.empty(B, K, H, H, dtype=torch.float16, device=DEV)
+                    lib.nova_forward(handles[i], x.data_ptr(), y.data_ptr(), B, H, H, 1)
+                    _check()
+                    outs[i].append(y)
+        for s in streams:
+            s.synchronize()
+    finally:
+        for h in handles:
+            lib.nova_destroy(h)
+    for i in range(2):
+        for y in outs[i]:
+            assert torch.equal(y, ref[i]), i
