@@ -223,10 +223,14 @@ def _grad_input_nova(holder, go, weight, padding, dtype):
         hd = _Handle()
         holder._bwd_handle = hd
     hd.set_stream(go.device)
+    # the flipped filter is cached for this exact weight tensor (weak
+    # reference: a freed tensor whose memory is reused can never match) at
+    # this version and storage
     key = (weight.data_ptr(), weight._version, tuple(weight.shape), weight.dtype)
-    if hd.key != key:
+    ref = hd.key
+    if not (ref is not None and ref[0]() is weight and ref[1] == key):
         hd.set_weights(weight.detach().flip(2, 3).transpose(0, 1))
-        hd.key = key
+        hd.key = (weakref.ref(weight), key)
     g16 = go.to(torch.float16).contiguous()
     B, K, Ho, Wo = g16.shape
     C = weight.shape[1]
@@ -378,6 +382,9 @@ class NovaWinogradConv2d(nn.Module):
         self._state = None
         if self._handle is not None:
             self._handle.key = None
+        bwd = getattr(self, "_bwd_handle", None)  # the flipped filter of the backward
+        if bwd is not None:
+            bwd.key = None
 
     def _apply(self, fn, *args, **kwargs):
         out = super()._apply(fn, *args, **kwargs)

@@ -86,3 +86,42 @@ def test_custom_op_caches_filter_transform(monkeypatch):
     assert len(calls) == n_same + 2
     assert torch.equal(y3, y4)
     assert not torch.equal(y1, y3)
+
+
+def test_grad_input_follows_weight_updates():
+    """The backward's flipped-filter transform is cached per weight tensor:
+    an in-place update (optimizer step), a rebound weight and a ``.data``
+    write followed by invalidate_weight_cache() are all picked up; each grad
+    input equals a fresh module's with the same weights, bit for bit."""
+    from nova_winograd import NovaWinogradConv2dTrainable
+
+    torch.manual_seed(13)
+    conv = NovaWinogradConv2dTrainable(16, 24, kernel_size=3, padding=1).to(DEV)
+    x = torch.randn(2, 16, 12, 12, device=DEV).half()
+
+    def grad_input(module):
+        xi = x.clone().requires_grad_(True)
+        y = module(xi)
+        y.backward(torch.ones_like(y))
+        torch.cuda.synchronize()
+        return xi.grad.clone()
+
+    def fresh():
+        m = NovaWinogradConv2dTrainable(16, 24, kernel_size=3, padding=1).to(DEV)
+        with torch.no_grad():
+            m.weight.copy_(conv.weight)
+        return m
+
+    g0 = grad_input(conv)
+    assert torch.equal(g0, grad_input(fresh()))
+    with torch.no_grad():
+        conv.weight.mul_(-0.5)  # in place: version bump
+    g1 = grad_input(conv)
+    assert torch.equal(g1, grad_input(fresh())) and not torch.equal(g1, g0)
+    conv.weight = torch.nn.Parameter(torch.randn(24, 16, 3, 3, device=DEV) * 0.1)  # rebound
+    g2 = grad_input(conv)
+    assert torch.equal(g2, grad_input(fresh()))
+    conv.weight.data.mul_(3.0)  # through .data: no version bump
+    conv.invalidate_weight_cache()
+    g3 = grad_input(conv)
+    assert torch.equal(g3, grad_input(fresh())) and not torch.equal(g3, g2)
