@@ -34,13 +34,14 @@ from nova_winograd.ops import (
 
 
 def _weight_key(weight):
-    """Identity of the weight contents the cached filter transform was built
-    from. ``_version`` catches in-place updates (optimizer steps,
-    ``load_state_dict``); object identity, pointer, dtype and shape catch
+    """State of the weight contents the cached filter transform was built
+    from, checked together with the weight object's identity (held by weak
+    reference). ``_version`` catches in-place updates (optimizer steps,
+    ``load_state_dict``); identity, pointer, dtype and shape catch
     re-binding, ``.to()`` and ``.half()``. (The reference keys on ``_version``
     alone, /root/reference/nova_winograd/conv2d.py:195-203.)"""
-    return (id(weight), weight._version, weight.data_ptr(), weight.dtype,
-            tuple(weight.shape), weight.device)
+    return (weight._version, weight.data_ptr(), weight.dtype, tuple(weight.shape),
+            weight.device)
 
 
 _FASTCALL = []  # [forward_ws or None], resolved once
@@ -405,9 +406,10 @@ class NovaWinogradConv2d(nn.Module):
         hd = self._handle
         hd.set_stream(self.weight.device)
         key = _weight_key(self.weight)
-        if key != hd.key:
+        ref = hd.key
+        if not (ref is not None and ref[0]() is self.weight and ref[1] == key):
             hd.set_weights(self.weight)
-            hd.key = key
+            hd.key = (weakref.ref(self.weight), key)
             self._weight_version = self.weight._version
             self._V_gemm = None
             self._M_gemm = None

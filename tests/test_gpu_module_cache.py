@@ -2,7 +2,8 @@
 same input shape, weight and bias (same objects, same versions, same storage)
 on the same stream only allocate the output and launch. Every change that
 the cache keys on must send the next call back through the full path: an
-in-place weight update, a weight re-bound through ``.data``, a new bias, a
+in-place weight update, a weight re-bound through ``.data``, a new weight
+Parameter, a new bias, a
 new input shape and a different current stream. Each result is compared
 bitwise with a freshly built module holding the same parameters.
 """
@@ -51,6 +52,10 @@ def test_cached_forward_invalidation():
         conv.weight.data = torch.randn(24, 16, 3, 3, device=DEV)  # new storage, no bump
         y3 = conv(x)
         assert torch.equal(y3, _fresh(conv)(x))
+
+        conv.weight = torch.nn.Parameter(torch.randn(24, 16, 3, 3, device=DEV))  # new object
+        y3b = conv(x)
+        assert torch.equal(y3b, _fresh(conv)(x))
 
         conv.bias = torch.nn.Parameter(torch.randn(24, device=DEV))  # new bias object
         y4 = conv(x)
