@@ -16,8 +16,9 @@
 //     copied into LDS as 16-byte-aligned row spans (anchored at the block's
 //     first column, image borders masked on read); the next chunk's loads are
 //     issued before the current chunk's arithmetic;
-//   * products: v_mfma_f32_16x16x16_f16 with V from LDS (B-fragment layout)
-//     and U from its fragment-ordered copy (one 512-byte read per fragment);
+//   * products: one v_mfma_f32_16x16x32_f16 per chunk, position and row
+//     tile, V from LDS and U from its fragment-ordered copy (1 KB contiguous
+//     per wave load);
 //   * M, rounded to fp16 (the reference's rounding point,
 //     nova_winograd_fused.hip:405), goes to a scratch buffer with agent-scope
 //     (write-through) stores; each workgroup waits for its stores to complete
@@ -27,7 +28,7 @@
 //     it also returns the counter to zero, so every launch finds the counters
 //     at zero. Nobody waits on another workgroup.
 // Both transforms use the shared tile arithmetic (bit-identical to the
-// standalone kernels); products accumulate over 16-channel steps in order.
+// standalone kernels); products accumulate over 32-channel chunks in order.
 #include <algorithm>
 
 #include "nova_internal.h"
@@ -62,7 +63,7 @@ struct FusedArgs {
     int C, K, Cp, H, W, pad, nh, nw, Ho, Wo;
     int tbh, tbw, nbh, nbw, n_kb;
     int rr, rp, cp, nj;  // staging geometry: rows, row pitch, channel pitch (bytes), loads/row
-    int nkt, nks;        // 16-row tiles / 16-channel steps of the fragment-ordered U
+    int nkt, nkp;        // 16-row tiles / 32-channel chunks of the fragment-ordered U
     const _Float16* bias;  // output epilogue (null: none)
     int relu;
     const _Float16* residual;  // added after the bias, y's layout (null: none)
@@ -72,11 +73,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 
-// V row layout (halves): [position q][k-step][channel group][tile][4 channels]:
-// the 16x16x16 B fragment of lane l (tile l % 16, channels 4*(l/16)..+3 of a
-// 16-channel step) is one conflict-free 8-byte read.
+// V row layout (halves): [position q][channel group][tile][16-channel half of
+// the chunk][4 channels]: the B operand of lane l (tile l % 16, channels
+// 4*(l/16)..+3 of both halves, paired like the fragment-ordered U) is one
+// 16-byte read.
 __device__ __forceinline__ int v_slot(int q, int c, int t) {
-    return (((q * 2 + (c >> 4)) * 4 + ((c >> 2) & 3)) * 16 + t) * 4 + (c & 3);
+    return (((q * 4 + ((c >> 2) & 3)) * 16 + t) * 2 + ((c >> 4) & 1)) * 4 + (c & 3);
 }
 
 // Row I of V for one (channel, tile) patch out of the staged rows. rb: LDS
@@ -252,21 +254,18 @@ __global__ __launch_bounds__(kFThreads, 1) void fused_kernel(FusedArgs a) {
     for (int c0 = 0; c0 < a.Cp; c0 += kFCC) {
         __syncthreads();  // previous chunk is done with xs and vs
         stage_store(c0);
-        // -- U fragments of this chunk: 2 positions x NM row tiles x 2 k-steps --
-        h4 ua[2][2][NM];
+        // -- U operands of this chunk: 2 positions x NM row tiles --
+        h8 ua[2][NM];
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
             const int p = 8 * i + 2 * wave + qq;
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    const int kt = kt0 + m, kst = (c0 >> 4) + ks;
-                    const int soff =
-                        (kt < a.nkt && kst < a.nks) ? ((p * a.nkt + kt) * a.nks + kst) * 512 : kFOob;
-                    ua[qq][ks][m] = __builtin_bit_cast(
-                        h4, __builtin_amdgcn_raw_buffer_load_b64(urs, lane * 8, soff, 0));
-                }
+            for (int m = 0; m < NM; m++) {
+                const int kt = kt0 + m;
+                const int soff = kt < a.nkt ? ((p * a.nkt + kt) * a.nkp + (c0 >> 5)) * 1024 : kFOob;
+                ua[qq][m] = __builtin_bit_cast(
+                    h8, __builtin_amdgcn_raw_buffer_load_b128(urs, lane * 16, soff, 0));
+            }
         }
         __syncthreads();
         if (c0 + kFCC < a.Cp) stage_load(c0 + kFCC);  // next chunk's rows, in flight
@@ -291,15 +290,11 @@ __global__ __launch_bounds__(kFThreads, 1) void fused_kernel(FusedArgs a) {
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
             const int q = 2 * wave + qq;
+            const h8 bv = *reinterpret_cast<const h8*>(vs + (q * 64 + lane) * 8);
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                const h4 bv = *reinterpret_cast<const h4*>(
-                    vs + (((q * 2 + ks) * 4 + (lane >> 4)) * 16 + (lane & 15)) * 4);
-#pragma unroll
-                for (int m = 0; m < NM; m++)
-                    acc[qq][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(ua[qq][ks][m], bv,
-                                                                       acc[qq][m], 0, 0, 0);
-            }
+            for (int m = 0; m < NM; m++)
+                acc[qq][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[qq][m], bv, acc[qq][m], 0,
+                                                                    0, 0);
         }
     }
 
@@ -487,7 +482,7 @@ hipError_t launch_fused(const uint16_t* x, const uint16_t* Uf, uint16_t* y, uint
     a.cp = p.cp;
     a.nj = p.nj;
     a.nkt = (K + 15) / 16;
-    a.nks = (Cp + 15) / 16;
+    a.nkp = (Cp + 31) / 32;
     const dim3 grid((unsigned)p.grid), block(kFThreads);
     switch (p.nm) {
         case 1: launch(fused_kernel<1>, grid, block, s, a); break;

@@ -15,15 +15,16 @@
 //   * per 32-channel chunk the input rows that the run touches are staged in
 //     LDS as 16-byte-aligned row spans; every thread transforms one (channel,
 //     tile) patch (the full 8x8, 40 aligned LDS reads) and writes its 64
-//     positions into a V buffer laid out as v_mfma_f32_16x16x16_f16 B
-//     fragments (one conflict-free 8-byte read per lane and position);
+//     positions into a V buffer laid out as v_mfma_f32_16x16x32_f16 B
+//     operands (one 16-byte read per lane and position);
 //   * each wave then multiplies its 8 positions: U fragments (A operands)
-//     straight from global/L2, two 16-channel k-steps per chunk;
+//     straight from global/L2, the chunk's two 16-channel fragments paired
+//     into one v_mfma_f32_16x16x32_f16 per (position, row tile);
 //   * after the channel loop, M (rounded to fp16, the reference's rounding
 //     point, nova_winograd_fused.hip:405) goes to LDS as [k][tile][position],
 //     and every thread runs the output transform for 2 (k, tile) pairs.
 // The transforms are the shared tile arithmetic (bit-identical to the
-// standalone kernels); products accumulate over 16-channel steps in order.
+// standalone kernels); products accumulate over 32-channel chunks in order.
 #include <algorithm>
 
 #include "nova_internal.h"
@@ -62,7 +63,7 @@ struct BlockArgs {
     int cp;       // bytes per staged channel
     int nj;       // 16-byte loads per row span
     int chan2;    // (2*H*W) mod 16: span-alignment step per channel
-    int nkt, nks; // 16-row output tiles and 16-channel steps of the fragment-ordered U
+    int nkt, nkp; // 16-row output tiles and 32-channel chunks of the fragment-ordered U
     int y_pairs;  // 1: store output pairs as 4-byte words (even Wo, 4-byte aligned y)
     const _Float16* bias;  // output epilogue (null: none)
     int relu;
@@ -74,30 +75,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 
-// V layout in LDS (halves): [position][k-step of 16 channels][channel group
-// of 4][tile][4 channels] -- the v_mfma_f32_16x16x16_f16 B fragment of lane l
-// (tile l % 16, channels 4*(l/16) .. +3) is one conflict-free 8-byte read.
+// V layout in LDS (halves): [position][channel group of 4][tile][16-channel
+// half of the chunk][4 channels] -- the B operand of lane l (tile l % 16,
+// channels 4*(l/16) .. +3 of both halves, paired like the A operands of the
+// fragment-ordered U) is one 16-byte read, 1 KB contiguous per wave.
 __device__ __forceinline__ int v_index(int pos, int c, int t) {
-    return (((pos * 2 + (c >> 4)) * 4 + ((c >> 2) & 3)) * 16 + t) * 4 + (c & 3);
+    return (((pos * 4 + ((c >> 2) & 3)) * 16 + t) * 2 + ((c >> 4) & 1)) * 4 + (c & 3);
 }
 
-// U fragments (A operands) of position row I at 16-channel step ks: 8
-// positions x 4 row tiles, read from the fragment-ordered copy of U (one
-// 512-byte contiguous fragment per wave load; zero padding built in). The
-// lane offset is the same for every fragment, the rest is a scalar offset.
-__device__ __forceinline__ void load_u(const BlockArgs& a, const __amdgpu_buffer_rsrc_t& urs,
-                                       int I, int kt0, int ks, int lane, h4 ua[8][4]) {
-#pragma unroll
-    for (int s = 0; s < 8; s++) {
-        const int p = 8 * I + s;
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++) {
-            const int kt = kt0 + kb;
-            const int soff = kt < a.nkt ? ((p * a.nkt + kt) * a.nks + ks) * 512 : kBOob;
-            ua[s][kb] = __builtin_bit_cast(
-                h4, __builtin_amdgcn_raw_buffer_load_b64(urs, lane * 8, soff, 0));
-        }
-    }
+// Byte offset of the A operand of (position p, row tile kt, chunk j) in the
+// fragment-ordered U; out of range (reads zero) past the last row tile.
+__device__ __forceinline__ int u_off(const BlockArgs& a, int p, int kt, int j) {
+    return kt < a.nkt ? ((p * a.nkt + kt) * a.nkp + j) * 1024 : kBOob;
 }
 
 // kNhwc: x and y channels-last. The chunk is then staged as [row][pixel]
@@ -286,44 +275,47 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 },
                 [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
         }
-        // half of the first k-step's U fragments (positions 0..3 of this
-        // wave's row) are requested before the barrier, so their L2 latency
-        // overlaps the wait for the slowest wave's transform (all of them
-        // would not fit beside the accumulators without spilling)
-        h4 ua0[4][4];
+        // the U operands of the first two positions of this wave's row are
+        // requested before the barrier, so their L2 latency overlaps the wait
+        // for the slowest wave's transform (more would not fit beside the
+        // accumulators without spilling)
+        h8 ua0[2][4];
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int s = 0; s < 2; s++)
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                const int kt = k0 / 16 + kb;
-                const int soff =
-                    kt < a.nkt ? (((8 * wave + s) * a.nkt + kt) * a.nks + (c0 >> 4)) * 512 : kBOob;
+            for (int kb = 0; kb < 4; kb++)
                 ua0[s][kb] = __builtin_bit_cast(
-                    h4, __builtin_amdgcn_raw_buffer_load_b64(urs, lane * 8, soff, 0));
-            }
+                    h8, __builtin_amdgcn_raw_buffer_load_b128(
+                            urs, lane * 16, u_off(a, 8 * wave + s, k0 / 16 + kb, c0 >> 5), 0));
         __syncthreads();
-        // -- products: this wave's position row, two 16-channel k-steps --
+        // -- products: this wave's position row, one v_mfma_f32_16x16x32_f16
+        // per (position, row tile) and chunk, positions in two halves of 4
+        // (64 registers of U operands beside the accumulators) --
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            h4 ua[8][4];
-            load_u(a, urs, wave, k0 / 16, (c0 >> 4) + ks, lane, ua);
-            if (ks == 0) {  // positions 0..3 already loaded
+        for (int half = 0; half < 2; half++) {
+            h8 ua[4][4];
 #pragma unroll
-                for (int s = 0; s < 4; s++)
+            for (int s = 0; s < 4; s++)
 #pragma unroll
-                    for (int kb = 0; kb < 4; kb++) ua[s][kb] = ua0[s][kb];
-            }
-            h4 vf[8];
+                for (int kb = 0; kb < 4; kb++) {
+                    if (half == 0 && s < 2) {
+                        ua[s][kb] = ua0[s][kb];
+                    } else {
+                        ua[s][kb] = __builtin_bit_cast(
+                            h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                    urs, lane * 16,
+                                    u_off(a, 8 * wave + 4 * half + s, k0 / 16 + kb, c0 >> 5), 0));
+                    }
+                }
 #pragma unroll
-            for (int s = 0; s < 8; s++)
-                vf[s] = *reinterpret_cast<const h4*>(
-                    vs + ((((8 * wave + s) * 2 + ks) * 4 + (lane >> 4)) * 16 + (lane & 15)) * 4);
-#pragma unroll
-            for (int s = 0; s < 8; s++)
+            for (int s = 0; s < 4; s++) {
+                const int pos = 8 * wave + 4 * half + s;
+                const h8 vb = *reinterpret_cast<const h8*>(vs + (pos * 64 + lane) * 8);
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
-                    acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ua[s][kb], vf[s],
-                                                                       acc[s][kb], 0, 0, 0);
+                    acc[4 * half + s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        ua[s][kb], vb, acc[4 * half + s][kb], 0, 0, 0);
+            }
         }
     }
     __syncthreads();  // staging area and V become M
@@ -492,7 +484,7 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.U = reinterpret_cast<const _Float16*>(U);
     a.u_bytes = (int)(2 * u_frag_elems(K, Cp));
     a.nkt = (K + 15) / 16;
-    a.nks = (Cp + 15) / 16;
+    a.nkp = (Cp + 31) / 32;
     a.y = reinterpret_cast<_Float16*>(y);
     a.y_bytes = (int)(2 * (int64_t)B * K * Ho * Wo);
     a.C = C;

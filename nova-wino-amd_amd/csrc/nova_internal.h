@@ -68,14 +68,18 @@ hipError_t launch_filter_transform_ref(const float* w, uint16_t* U, int K, int C
 hipError_t launch_filter_transform_gemm(const void* w, bool w_f16, uint16_t* U, int K, int C,
                                         int Cp, hipStream_t s);
 
-// Fragment-ordered copy of U for the fused kernels: for each position p, 16-row
-// output-channel tile kt and 16-channel step ks, the v_mfma_f32_16x16x16_f16 A
-// fragment as 64 lanes x 4 halves (lane = row + 16 * (channel % 16 / 4)), so a
-// wave reads one fragment as 512 contiguous bytes. Rows >= K and channels >= C
-// are zero. Uf[((p*nkt + kt)*nks + ks)*256 + lane*4 + e], nkt = ceil(K/16),
-// nks = ceil(Cp/16).
+// Fragment-ordered copy of U for the fused kernels: for each position p,
+// 16-row output-channel tile kt and 32-channel chunk j, one
+// v_mfma_f32_16x16x32_f16 A operand per lane, 64 lanes x 8 halves, so a wave
+// reads it as 1024 contiguous bytes (16 per lane). Lane l holds row
+// 16*kt + l % 16 and channels 32*j + 16*ks + 4*(l / 16) + e for ks = 0, 1
+// and e = 0..3 in that order: the two 16-channel halves of the chunk that a
+// 16x16x16 fragment would put in lane l, side by side (a B operand built the
+// same way pairs every channel with itself). Rows >= K and channels >= Cp are
+// zero. Uf[((p*nkt + kt)*nkp + j)*512 + l*8 + ks*4 + e], nkt = ceil(K/16),
+// nkp = ceil(Cp/32).
 inline int64_t u_frag_elems(int K, int Cp) {
-    return (int64_t)64 * ((K + 15) / 16) * ((Cp + 15) / 16) * 256;
+    return (int64_t)64 * ((K + 15) / 16) * ((Cp + 31) / 32) * 512;
 }
 hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStream_t s);
 

@@ -87,20 +87,21 @@ hipError_t launch_filter_transform_gemm(const void* w, bool w_f16, uint16_t* U, 
     return hipGetLastError();
 }
 
-// Reorder U[p][k][Cp] into MFMA A-fragment order (zero padded), one thread per
-// 4-channel lane slot.
+// Reorder U[p][k][Cp] into the fused kernels' A-operand order (zero padded),
+// one thread per 4-channel slot (lane, half ks) of a fragment.
 __global__ __launch_bounds__(256) void u_frag_kernel(const _Float16* __restrict__ U,
                                                       _Float16* __restrict__ Uf, int K, int Cp,
-                                                      int nkt, int nks, int64_t nslots) {
+                                                      int nkt, int nkp, int64_t nslots) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nslots) return;
-    const int lane = (int)(i & 63);
-    const int64_t frag = i >> 6;  // (p*nkt + kt)*nks + ks
-    const int ks = (int)(frag % nks);
-    const int kt = (int)((frag / nks) % nkt);
-    const int p = (int)(frag / ((int64_t)nks * nkt));
+    const int ks = (int)(i & 1);
+    const int lane = (int)((i >> 1) & 63);
+    const int64_t frag = i >> 7;  // (p*nkt + kt)*nkp + j
+    const int j = (int)(frag % nkp);
+    const int kt = (int)((frag / nkp) % nkt);
+    const int p = (int)(frag / ((int64_t)nkp * nkt));
     const int k = kt * 16 + (lane & 15);
-    const int c = ks * 16 + 4 * (lane >> 4);
+    const int c = j * 32 + ks * 16 + 4 * (lane >> 4);
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     h4 v = {(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
     if (k < K && c < Cp) v = *reinterpret_cast<const h4*>(U + ((int64_t)p * K + k) * Cp + c);
@@ -108,10 +109,10 @@ __global__ __launch_bounds__(256) void u_frag_kernel(const _Float16* __restrict_
 }
 
 hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStream_t s) {
-    const int nkt = (K + 15) / 16, nks = (Cp + 15) / 16;
-    const int64_t nslots = (int64_t)64 * nkt * nks * 64;
+    const int nkt = (K + 15) / 16, nkp = (Cp + 31) / 32;
+    const int64_t nslots = (int64_t)64 * nkt * nkp * 128;
     launch(u_frag_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), s,
-        reinterpret_cast<const _Float16*>(U), reinterpret_cast<_Float16*>(Uf), K, Cp, nkt, nks,
+        reinterpret_cast<const _Float16*>(U), reinterpret_cast<_Float16*>(Uf), K, Cp, nkt, nkp,
         nslots);
     return hipGetLastError();
 }

@@ -85,10 +85,14 @@ def test_auto_path_matches_three_pass(oracle, B, C, K, H, expect):
         assert np.array_equal(y_auto.cpu().view(torch.int16).numpy(),
                               y_3p.cpu().view(torch.int16).numpy())
     else:
-        # same transforms, GEMM accumulated in 16- instead of 32-channel steps
+        # same transforms; the products are summed in another fp32 order
+        # (32-channel chunks with the channels of an MFMA permuted, against
+        # 64-channel stages), so an M value near an fp16 rounding boundary can
+        # round one ulp apart: at |M| < 128 that is 0.0625, which the output
+        # transform weights by at most |A[r][q]·A[c][p]| < 4.8 -> 0.3
         rel = np.linalg.norm(a - r) / np.linalg.norm(r)
         assert rel <= 2e-3, rel
-        assert np.abs(a - r).max() <= 0.1
+        assert np.abs(a - r).max() <= 0.3
     # the first two images against the oracle
     yo = oracle.conv2d(x[:2].numpy(), w.numpy(), 1)
     assert oracle.rel_l2(a[:2].astype(np.float16), yo) <= 5e-3
