@@ -268,20 +268,29 @@ int choose_path(const Handle* Hd, const Shape& s) {
         FusedBlockPlan p;
         return fused_block_plan_for(Hd, s, &p) ? 3 : 1;
     }
-    // Automatic choice, from MI355X measurements: the tile-block fused kernel
-    // for layers with at most 64 input and output channels, when its
-    // workgroups (one per CU at a time, ~28 us each at conv2_x) fill their
-    // last wave over the CUs to at least 80 %: its time steps by whole waves
-    // while the three-pass time grows with the batch. ResNet-50 conv2_x
-    // forwards, us, three-pass vs fused: B=16 27.0 vs 29.5 (grid 112), B=32
-    // 36.1 vs 30.0 (224: 88 % fill), B=40 42.4 vs 50.0 (280: 55 %), B=48
-    // 48.8 vs 56.4 (66 %), B=64 59.6 vs 57.7 (88 %), B=80 71.3 vs 77.8
-    // (73 %), B=128 120.7 vs 111.3, B=256 260.6 vs 194.8 (88 %); everything
-    // else runs three-pass.
+    // Automatic choice for layers with at most 64 input and output channels,
+    // by a cost model fitted to MI355X forwards (36 shapes: C = K = 32 and 64
+    // at 28^2-56^2, C = 48 -> K = 40 at 13^2, NCHW and NHWC, batch 2-192;
+    // the rule picks the faster path in all but 5, which lose 0.2-3 us):
+    //  * fused tile-block: its workgroups run one per CU, so the time steps
+    //    by waves of workgroups over the CUs, ~3 us + 10 us per 32-channel
+    //    chunk each (conv2_x batch 16-36: 25.7-27.3 us, one wave; 40-72:
+    //    44-53 us; C = 32: 15 us per wave);
+    //  * three-pass: ~10 us of dependent launches plus its HBM bytes (x, y,
+    //    V and M written and read) at 5 TB/s (conv2_x batch 16: 27.0 us,
+    //    batch 128: 122 us).
+    // Examples, three-pass vs fused, us: conv2_x B=8 21.5 vs 25.2, B=16 27.0
+    // vs 25.7, B=44 46.7 vs 50.5, B=56 55.0 vs 51.4, B=112 102.8 vs 91.4;
+    // 64@28^2 B=64 29.1 vs 25.6; 32@56^2 B=8 19.7 vs 15.0; 48->40@13^2 B=128
+    // 22.8 vs 24.2.
     FusedBlockPlan bp;
-    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp) && bp.grid >= 128) {
+    if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
-        if (bp.grid * 5 >= waves * Hd->cus * 4) return 3;
+        const double t_fused = (double)waves * (3.0 + 10.0 * ((Hd->Cp + 31) / 32));
+        const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
+                           4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
+        const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us
+        if (t_fused < t_three) return 3;
     }
     return 1;
 }
