@@ -79,6 +79,14 @@ def kernel_alg_bytes(kind, B, C, K, H):
     return {"input": x + V, "gemm": U + V + M, "output": M + y, "fused": x + U + y}[kind]
 
 
+def kernel_alg_flops(kind, B, C, K, H):
+    """Algorithmic MFMA FLOPs of one launch: the 64 Winograd-domain products,
+    2*64*K*C*BP at minimal tiling (GEMM and fused kinds; the transforms are
+    VALU work and count 0)."""
+    BP = B * (-(-H // 6)) ** 2
+    return 2.0 * 64 * K * C * BP if kind in ("gemm", "fused") else 0.0
+
+
 def time_region(fn, reps, torch):
     """Mean ms per call over `reps` calls, CUDA events on the current stream."""
     s = torch.cuda.Event(enable_timing=True)
@@ -124,6 +132,22 @@ def load_traffic(kernel_name):
     for rec in data.get("kernels", []):
         if rec.get("kernel") == kernel_name:
             return rec.get("hbm_bytes_per_launch")
+    return None
+
+
+def load_mfma(kernel_name):
+    """Executed MFMA FLOPs per launch (mean over the step's layers) of a kernel
+    family, measured offline with rocprofv3 SQ_INSTS_VALU_MFMA_MOPS_F16
+    (profiles/mfma.json), or None."""
+    path = os.path.join(ROOT, "profiles", "mfma.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    for rec in data.get("kernels", []):
+        if rec.get("kernel") == kernel_name:
+            return {k: rec[k] for k in ("executed_flops_per_launch", "alg_flops_per_launch",
+                                        "busy_per_512_flops") if k in rec}
     return None
 
 
@@ -173,37 +197,147 @@ def _name_keys(name):
     return [name.rstrip(">"), base + "I" + "".join(f"Li{a}E" for a in args)]
 
 
+def pmc_rows(d, counter):
+    """Per-dispatch means of one counter from the rocprofv3 --pmc database
+    under d: [(kernel name, grid size, mean value, dispatches)], grouped by
+    kernel name and grid size."""
+    import glob
+    import sqlite3
+
+    dbs = sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True))
+    if not dbs:
+        raise SystemExit(f"no rocprofv3 database under {d}")
+    con = sqlite3.connect(dbs[-1])
+    tabs = [r[0] for r in con.execute("select name from sqlite_master where type in "
+                                      "('table','view')")]
+    for t in tabs:
+        cols = [c[1] for c in con.execute(f"pragma table_info('{t}')")]
+        if {"kernel_name", "counter_name", "value"} <= set(cols):
+            gcol = "grid_size" if "grid_size" in cols else "grid_size_x"
+            rows = con.execute(f"select kernel_name, {gcol}, avg(value), count(*) from '{t}' "
+                               f"where counter_name = ? group by kernel_name, {gcol}",
+                               (counter,)).fetchall()
+            return rows, dbs[-1]
+    raise SystemExit(f"no counter table in {dbs[-1]}: {tabs}")
+
+
+MFMA_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_F16", "SQ_VALU_MFMA_BUSY_CYCLES")
+CLOCK_GHZ = 2.4  # MI355X peak engine clock (2.5 PFLOP/s = 256 CUs x 4 SIMDs x 1024 x 2.4 GHz)
+
+
+def mfma_from(pmc_dir, bench_json, out_path, cus=256):
+    """MFMA work of the library's product kernels from one rocprofv3 --pmc run
+    of `bench.py --pmc-mode` with MFMA_COUNTERS: executed fp16 MFMA FLOPs per
+    dispatch (SQ_INSTS_VALU_MFMA_MOPS_F16 counts multiply and add operations
+    in units of 512) and the matrix units' busy cycles summed over SIMDs
+    (SQ_VALU_MFMA_BUSY_CYCLES). Over each family's event-timed launch
+    duration in the unprofiled bench line (bench_json) they give the share of
+    the 2.5 PFLOP/s dense fp16 peak reached and the share of SIMD cycles the
+    matrix units were busy; busy cycles per 512 FLOPs tell the instruction's
+    rate (0.5 = the full dense rate of v_mfma_f32_16x16x32_f16)."""
+    with open(bench_json) as f:
+        line = json.loads([ln for ln in f if ln.startswith("{")][-1])
+    fams = line.get("kernel_families", {})
+    per = {c: pmc_rows(pmc_dir, c)[0] for c in MFMA_COUNTERS}
+    data = {"method": "rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " of bench.py --pmc-mode; "
+                      "executed FLOPs = 512 x SQ_INSTS_VALU_MFMA_MOPS_F16; busy share = "
+                      "SQ_VALU_MFMA_BUSY_CYCLES / (bench avg_launch_us x "
+                      f"{CLOCK_GHZ} GHz x {cus} CUs x 4 SIMDs)",
+            "peak_tflops": PEAK_FP16_TFLOPS, "clock_ghz": CLOCK_GHZ, "kernels": []}
+    for name in ("wgemm", "fused_block_kernel", "fused_kernel<1>", "fused_kernel<2>",
+                 "fused_kernel<4>"):
+        sel = {c: [r for r in per[c] if any(k in r[0] for k in _name_keys(name))]
+               for c in MFMA_COUNTERS}
+        mops = sel["SQ_INSTS_VALU_MFMA_MOPS_F16"]
+        if not mops:
+            continue
+        n = sum(r[3] for r in mops)
+        flops = sum(r[2] * r[3] for r in mops) / n * 512.0
+        busy_rows = sel["SQ_VALU_MFMA_BUSY_CYCLES"]
+        busy = (sum(r[2] * r[3] for r in busy_rows) / sum(r[3] for r in busy_rows)
+                if busy_rows else None)
+        bmap = {(r[0], r[1]): r[2] for r in busy_rows}
+        grids = [{"kernel": r[0], "grid": r[1], "dispatches": r[3],
+                  "executed_gflop": round(r[2] * 512.0 / 1e9, 4),
+                  "busy_cycles": round(bmap.get((r[0], r[1]), 0.0)),
+                  "busy_per_512_flops": (round(bmap[(r[0], r[1])] / r[2], 3)
+                                         if r[2] and (r[0], r[1]) in bmap else None)}
+                 for r in mops]
+        rec = {"kernel": name, "executed_flops_per_launch": round(flops), "by_grid": grids}
+        if busy is not None:
+            rec["busy_cycles_per_launch"] = round(busy)
+            rec["busy_per_512_flops"] = round(busy / (flops / 512.0), 3) if flops else None
+        fam = fams.get(name)
+        if fam and "alg_gflop_per_launch" in fam:
+            rec["alg_flops_per_launch"] = round(fam["alg_gflop_per_launch"] * 1e9)
+            rec["avg_launch_us"] = fam["avg_launch_us"]
+            tf = flops / (fam["avg_launch_us"] * 1e-6) / 1e12
+            rec["executed_tflops"] = round(tf, 1)
+            rec["frac_of_peak"] = round(tf / PEAK_FP16_TFLOPS, 4)
+            if busy is not None:
+                simd_cycles = fam["avg_launch_us"] * 1e-6 * CLOCK_GHZ * 1e9 * cus * 4
+                rec["mfma_busy_frac"] = round(busy / simd_cycles, 4)
+        data["kernels"].append(rec)
+    with open(out_path, "w") as f:
+        json.dump(data, f, indent=1)
+    write_mfma_summary(data, os.path.join(os.path.dirname(out_path),
+                                          "mfma_resnet50_3x3s1_b1_b32.md"))
+    print(json.dumps(data))
+
+
+def write_mfma_summary(data, path):
+    """Markdown summary of mfma.json."""
+    short = lambda n, k=60: (n[:k] + "…") if len(n) > k else n  # noqa: E731
+    lines = [
+        "# MFMA work per launch, product kernels, ResNet-50 3x3 s1 layers at B=1 and B=32",
+        "",
+        "Commands (from the repository root, on one MI355X):",
+        "",
+        "```",
+        "python3 -u bench.py --details out/bench_details.json > out/bench_line.json",
+        "cd /tmp && export TMPDIR=/tmp && cd -",
+        "timeout -s KILL 120 rocprofv3 --pmc " + " ".join(MFMA_COUNTERS)
+        + " -d out/pmc_mfma -o pmc -- python3 -u bench.py --pmc-mode",
+        "python3 bench.py --mfma-from out/pmc_mfma out/bench_line.json"
+        "   # -> profiles/mfma.json + this file",
+        "```",
+        "",
+        data["method"] + ".",
+        "",
+        "| kernel | grid (threads) | dispatches | executed GFLOP | MFMA busy cycles | "
+        "busy cycles per 512 FLOPs |",
+        "|---|---:|---:|---:|---:|---:|",
+    ]
+    for k in data["kernels"]:
+        for g in k["by_grid"]:
+            lines.append(f"| `{short(g['kernel'])}` | {g['grid']} | {g['dispatches']} | "
+                         f"{g['executed_gflop']} | {g['busy_cycles']} | "
+                         f"{g['busy_per_512_flops']} |")
+    lines += ["", "| family | executed GFLOP / launch | algorithmic GFLOP / launch | "
+                  "bench avg_launch_us | executed TFLOP/s | of 2.5 PFLOP/s | MFMA busy share |",
+              "|---|---:|---:|---:|---:|---:|---:|"]
+    for k in data["kernels"]:
+        alg = k.get("alg_flops_per_launch")
+        lines.append(f"| {k['kernel']} | {k['executed_flops_per_launch'] / 1e9:.4f} | "
+                     f"{(alg / 1e9) if alg else float('nan'):.4f} | {k.get('avg_launch_us')} | "
+                     f"{k.get('executed_tflops')} | {k.get('frac_of_peak')} | "
+                     f"{k.get('mfma_busy_frac')} |")
+    with open(path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
 def traffic_from(fetch_dir, write_dir, out_path):
     """HBM bytes per launch of each library kernel from two rocprofv3 --pmc runs
     of `bench.py --pmc-mode` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
     each scaled by the same counter's reading for the known-size copy kernel.
     The figure kept per kernel is the mean over the layers it ran on, the same
     averaging as the bench line's avg_launch_us."""
-    import glob
-    import sqlite3
-
     def read(d, counter):
-        dbs = sorted(glob.glob(os.path.join(d, "**", "*.db"), recursive=True))
-        if not dbs:
-            raise SystemExit(f"no rocprofv3 database under {d}")
-        con = sqlite3.connect(dbs[-1])
-        tabs = [r[0] for r in con.execute("select name from sqlite_master where type in "
-                                          "('table','view')")]
-        rows = None
-        for t in tabs:
-            cols = [c[1] for c in con.execute(f"pragma table_info('{t}')")]
-            if {"kernel_name", "counter_name", "value"} <= set(cols):
-                gcol = "grid_size" if "grid_size" in cols else "grid_size_x"
-                rows = con.execute(f"select kernel_name, {gcol}, avg(value), count(*) from '{t}' "
-                                   f"where counter_name = ? group by kernel_name, {gcol}",
-                                   (counter,)).fetchall()
-                break
-        if rows is None:
-            raise SystemExit(f"no counter table in {dbs[-1]}: {tabs}")
+        rows, db = pmc_rows(d, counter)
         copy = [r for r in rows if "copy" in r[0].lower() or "elementwise" in r[0].lower()]
         copy = [r for r in copy if r[2] > COPY_MIB * 1024 * 0.5]
         if not copy:
-            raise SystemExit(f"{counter}: calibration copy not found in {dbs[-1]}")
+            raise SystemExit(f"{counter}: calibration copy not found in {db}")
         copy_kib = min(copy, key=lambda r: abs(r[2] - COPY_MIB * 1024))[2]
         factor = COPY_MIB * 1024.0 / copy_kib
         per = {}
@@ -569,6 +703,9 @@ def main():
     ap.add_argument("--kernel-stats-from", nargs=2, metavar=("TRACE_DIR", "BENCH_JSON"),
                     help="write profiles/kernels_resnet50_3x3s1_b1_b32.md from a rocprofv3 "
                          "kernel-trace run and the unprofiled bench line")
+    ap.add_argument("--mfma-from", nargs=2, metavar=("PMC_DIR", "BENCH_JSON"),
+                    help="write profiles/mfma.json + its summary from a rocprofv3 --pmc run "
+                         "with the MFMA counters and a bench line")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two --pmc-mode profiles into profiles/traffic.json and exit")
     args = ap.parse_args()
@@ -580,6 +717,9 @@ def main():
     if args.traffic_from:
         traffic_from(args.traffic_from[0], args.traffic_from[1],
                      os.path.join(ROOT, "profiles", "traffic.json"))
+        return
+    if args.mfma_from:
+        mfma_from(args.mfma_from[0], args.mfma_from[1], os.path.join(ROOT, "profiles", "mfma.json"))
         return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -690,7 +830,9 @@ def main():
                                               "gbs": ab / (ev * 1e-3) / 1e9}
                 fam = FAMILY_OF_KIND.get(k, kname)
                 agg = kernels.setdefault(fam, {"ms": 0.0, "replay_ms": 0.0, "launches": 0,
-                                               "bytes": 0.0, "by_layer": [], "members": {}})
+                                               "bytes": 0.0, "flops": 0.0, "by_layer": [],
+                                               "members": {}})
+                agg["flops"] += kernel_alg_flops(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"])
                 agg["members"][kname] = agg["members"].get(kname, 0) + 1
                 agg["ms"] += ev
                 agg["replay_ms"] += per
@@ -739,6 +881,14 @@ def main():
         "share_of_kernel_time": round(dom["ms"] / sum(v["ms"] for v in kernels.values()), 3),
         "layers": dom_desc,
     }
+    if dom["flops"] > 0:
+        # the same launches against the dense fp16 MFMA peak (algorithmic
+        # FLOPs; profiles/mfma.json holds the executed ones from the counters)
+        tf = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+        roofline["mfma"] = {"achieved": round(tf, 1), "peak": PEAK_FP16_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(tf / PEAK_FP16_TFLOPS, 4),
+                            "alg_flops_per_launch": round(dom["flops"] / dom["launches"]),
+                            "counters": load_mfma(dom_name)}
 
     families = {
         fam: {"avg_launch_us": round(v["ms"] / v["launches"] * 1e3, 3),
@@ -747,6 +897,12 @@ def main():
               "achieved_gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
               "frac_hbm": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         for fam, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])}
+    for fam, v in kernels.items():
+        if v["flops"] > 0:
+            tf = v["flops"] / (v["ms"] * 1e-3) / 1e12
+            families[fam].update({"alg_gflop_per_launch": round(v["flops"] / v["launches"] / 1e9, 4),
+                                  "achieved_tflops": round(tf, 1),
+                                  "frac_mfma": round(tf / PEAK_FP16_TFLOPS, 4)})
 
     layers_out = []
     for r in runs:

@@ -139,3 +139,50 @@ def test_bench_kernel_stats_summary(tmp_path):
     text = out.read_text()
     assert "| wgemm | 11.000 | 10.000 | 4 | 1.100 |" in text
     assert "| input_transform_kernel | 5.500 | 5.000 | 4 | 1.100 |" in text
+
+
+def test_bench_mfma_summary(tmp_path):
+    """bench.py's MFMA counter summary: executed FLOPs from
+    SQ_INSTS_VALU_MFMA_MOPS_F16 (x 512), busy cycles per 512 FLOPs, and the
+    peak and busy shares over the bench line's event-timed launch (synthetic
+    database with the columns rocprofv3's counter table has)."""
+    import importlib.util
+    import json
+    import os
+    import sqlite3
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    d = tmp_path / "pmc"
+    d.mkdir()
+    con = sqlite3.connect(d / "pmc_results.db")
+    con.execute("create table counters (kernel_name text, grid_size int, counter_name text, "
+                "value real)")
+    g = "_ZN4nova16wgemm_lds_kernelILi64E"
+    rows = []
+    for grid, mops in ((1024, 1000.0), (2048, 3000.0)):
+        for _ in range(2):
+            rows += [(g, grid, "SQ_INSTS_VALU_MFMA_MOPS_F16", mops),
+                     (g, grid, "SQ_VALU_MFMA_BUSY_CYCLES", 0.5 * mops)]
+    rows.append(("_ZN4nova22input_transform_kernelILi2E", 256, "SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0))
+    con.executemany("insert into counters values (?,?,?,?)", rows)
+    con.commit()
+    con.close()
+    line = {"kernel_families": {"wgemm": {"avg_launch_us": 2.048,
+                                          "alg_gflop_per_launch": 0.001}}}
+    bl = tmp_path / "line.json"
+    bl.write_text(json.dumps(line) + "\n")
+    out = tmp_path / "mfma.json"
+    bench.mfma_from(str(d), str(bl), str(out), cus=4)
+    data = json.loads(out.read_text())
+    (rec,) = data["kernels"]
+    assert rec["kernel"] == "wgemm"
+    assert rec["executed_flops_per_launch"] == 2000 * 512
+    assert rec["busy_per_512_flops"] == 0.5
+    assert rec["busy_cycles_per_launch"] == 1000
+    assert rec["mfma_busy_frac"] == pytest.approx(1000 / (2.048e-6 * 2.4e9 * 16), abs=1e-4)
+    assert rec["executed_tflops"] == pytest.approx(2000 * 512 / 2.048e-6 / 1e12, abs=0.1)
+    assert rec["alg_flops_per_launch"] == 1000000
+    assert "| wgemm |" in (tmp_path / "mfma_resnet50_3x3s1_b1_b32.md").read_text()
