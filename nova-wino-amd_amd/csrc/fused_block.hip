@@ -44,6 +44,7 @@ typedef unsigned u4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBT = 512;                            // threads per workgroup (8 waves)
 constexpr int kBCC = 32;                            // channels per chunk
+constexpr int kPre = 4;                             // positions of U operands prefetched
 constexpr int kBMPitch = 72;                        // halves per (k, tile) row of M
 constexpr int kBLdsBytes = 160 * 1024;              // whole LDS: staging + V, later M
 constexpr int kBVBytes = 64 * kBCC * 16 * 2;        // 65536: V of one chunk
@@ -275,13 +276,13 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 },
                 [&](int r, int s2, float v) { vs[v_index(r * 8 + s2, ct, t)] = to_f16(v); });
         }
-        // the U operands of the first two positions of this wave's row are
-        // requested before the barrier, so their L2 latency overlaps the wait
-        // for the slowest wave's transform (more would not fit beside the
-        // accumulators without spilling)
-        h8 ua0[2][4];
+        // the U operands of the first half of this wave's row (kPre
+        // positions) are requested before the barrier, so their L2 latency
+        // overlaps the wait for the slowest wave's transform (more would not
+        // fit beside the accumulators without spilling)
+        h8 ua0[kPre][4];
 #pragma unroll
-        for (int s = 0; s < 2; s++)
+        for (int s = 0; s < kPre; s++)
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
                 ua0[s][kb] = __builtin_bit_cast(
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
             for (int s = 0; s < 4; s++)
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++) {
-                    if (half == 0 && s < 2) {
+                    if (half == 0 && s < kPre) {
                         ua[s][kb] = ua0[s][kb];
                     } else {
                         ua[s][kb] = __builtin_bit_cast(
