@@ -103,6 +103,7 @@ struct Handle {
     size_t U_cap = 0;  // bytes
     uint16_t* Uf = nullptr;  // U in MFMA fragment order (fused kernels)
     size_t Uf_cap = 0;       // bytes
+    bool uf_ready = false;   // Uf holds the current weights' fragments
     void* ws = nullptr;
     size_t ws_cap = 0;  // bytes
     unsigned* cnt = nullptr;  // fused-kernel arrival counters, zero between launches
@@ -159,6 +160,29 @@ bool ensure_ws(Handle* H, size_t bytes) {
     if (!hip_ok(hipMalloc(&H->ws, want), "hipMalloc(workspace)")) return false;
     H->ws_cap = want;
     return true;
+}
+
+// The fragment-ordered copy of U that the fused kernels read, built from U
+// on the handle's stream the first time a fused path needs it for the
+// current weights (set_weights builds it at once when the automatic choice
+// can pick a fused kernel or one is forced, so a forward -- or a captured
+// graph -- normally finds it ready). Layers that always run three-pass never
+// hold it: for 1280 x 1280 channels that saves 210 MB per handle.
+bool ensure_uf(Handle* H) {
+    if (H->uf_ready) return true;
+    const size_t need = (size_t)u_frag_elems(H->K, H->Cp) * sizeof(uint16_t);
+    if (need > H->Uf_cap) {
+        if (H->Uf) {
+            if (!hip_ok(hipFree(H->Uf), "hipFree(Uf)")) return false;
+            H->Uf = nullptr;
+            H->Uf_cap = 0;
+        }
+        if (!hip_ok(hipMalloc(&H->Uf, need), "hipMalloc(Uf)")) return false;
+        H->Uf_cap = need;
+    }
+    H->uf_ready = hip_ok(launch_u_frag(H->U, H->Uf, H->K, H->Cp, H->stream),
+                         "filter fragment order");
+    return H->uf_ready;
 }
 
 // Counters of the fused kernel: zeroed once when (re)allocated; each launch
@@ -355,6 +379,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     if (path == 3 && Hd->nhwc && !aligned16(x)) path = 1;
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s_all));
     const bool fused = path == 2 || path == 3;
+    if (fused && !ensure_uf(Hd)) return;
     if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3)) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
@@ -500,19 +525,7 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
         }
         H->U_cap = need;
     }
-    const size_t need_f = (size_t)u_frag_elems(K, Cp) * sizeof(uint16_t);
-    if (need_f > H->Uf_cap) {
-        if (H->Uf) {
-            if (!hip_ok(hipFree(H->Uf), "hipFree(Uf)")) return;
-            H->Uf = nullptr;
-            H->Uf_cap = 0;
-        }
-        if (!hip_ok(hipMalloc(&H->Uf, need_f), "hipMalloc(Uf)")) {
-            H->ready = false;
-            return;
-        }
-        H->Uf_cap = need_f;
-    }
+    H->uf_ready = false;
     H->K = K;
     H->C = C;
     H->Cp = Cp;
@@ -522,8 +535,10 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
         cus > 0)
         H->cus = cus;
     H->ready = hip_ok(launch_filter_transform_gemm(d_weight, w_f16, H->U, K, C, Cp, H->stream),
-                      "filter transform") &&
-               hip_ok(launch_u_frag(H->U, H->Uf, K, Cp, H->stream), "filter fragment order");
+                      "filter transform");
+    const bool fused_possible = (C <= 64 && K <= 64 && H->path_pref == 0) ||
+                                H->path_pref == 2 || H->path_pref == 3;
+    if (H->ready && fused_possible) H->ready = ensure_uf(H);
 }
 
 }  // namespace
@@ -674,6 +689,7 @@ void nova_set_path(nova_handle_t h, int path) {
         return;
     }
     H->path_pref = path;
+    if ((path == 2 || path == 3) && H->ready) ensure_uf(H);  // fused forced after the weights
 }
 
 void nova_set_window_bytes(nova_handle_t h, long long bytes) {

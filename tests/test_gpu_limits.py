@@ -107,3 +107,57 @@ def test_image_over_budget_is_refused():
     finally:
         lib.nova_destroy(h)
     torch.cuda.synchronize()
+
+
+def test_fused_operands_built_only_when_a_fused_path_can_run():
+    """The fragment-ordered copy of U that the fused kernels read is built
+    only for handles that can run them: a 1280 x 1280 layer on the automatic
+    path holds U alone (210 MB); forcing a fused path after the weights builds
+    the copy (another 210 MB). A small layer forced onto the fused kernel
+    after its weights matches the three-pass result."""
+    from nova_winograd.ops import check, get_lib
+
+    lib = get_lib()
+    K = C = 1280
+    u_bytes = 64 * K * C * 2
+    w = torch.zeros(K, C, 3, 3, device=DEV)
+    torch.cuda.synchronize()
+    h = lib.nova_create()
+    try:
+        free0 = torch.cuda.mem_get_info()[0]
+        lib.nova_set_weights(h, w.data_ptr(), K, C)
+        check()
+        torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+        assert u_bytes <= free0 - free1 < 1.5 * u_bytes, (free0 - free1)
+        lib.nova_set_path(h, 3)
+        check()
+        torch.cuda.synchronize()
+        free2 = torch.cuda.mem_get_info()[0]
+        assert 0.9 * u_bytes <= free1 - free2 < 1.5 * u_bytes, (free1 - free2)
+    finally:
+        lib.nova_destroy(h)
+    del w
+    torch.cuda.synchronize()
+
+    B, C, K, H = 4, 96, 80, 12
+    print(f"[limits] fused forced after weights B={B} C={C} K={K} H={H}", flush=True)
+    torch.manual_seed(5)
+    x = torch.randn(B, C, H, H, device=DEV, dtype=torch.float16)
+    w = torch.randn(K, C, 3, 3, device=DEV) * 0.05
+    ys = {}
+    for path in (1, 3):
+        h = lib.nova_create()
+        try:
+            lib.nova_set_weights(h, w.data_ptr(), K, C)
+            lib.nova_set_path(h, path)
+            y = torch.empty(B, K, H, H, device=DEV, dtype=torch.float16)
+            lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, H, 1)
+            check()
+            assert lib.nova_get_last_path(h) == path
+            torch.cuda.synchronize()
+            ys[path] = y.float()
+        finally:
+            lib.nova_destroy(h)
+    rel = ((ys[3] - ys[1]).norm() / ys[1].norm()).item()
+    assert rel <= 2e-3, rel
