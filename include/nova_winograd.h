@@ -125,7 +125,11 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
  * (nova_set_window_bytes), each window's three kernels back to back -- the
  * BP-windowed pipeline of /root/reference/tests/test_bp_tiled.hip:482-571,
  * never chosen automatically. A forced fused path outside its envelope runs
- * 3-pass and reports an error. */
+ * 3-pass and reports an error. The fused kernels read a second, fragment-
+ * ordered copy of the transformed filter (device memory the size of U); a
+ * handle builds it in nova_set_weights when a fused kernel can run (C, K <= 64
+ * on the automatic path, or 2 / 3 already forced), here when 2 or 3 is forced
+ * after the weights, and otherwise never. */
 NOVA_API void nova_set_path(nova_handle_t h, int path);
 /* V + M bytes per window of path 4 (0 = default, 4 MiB, the reference's
  * budget; at least one image per window). No counterpart in the reference,
