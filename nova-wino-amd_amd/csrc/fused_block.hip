@@ -1,6 +1,7 @@
 // Fused NOVA F(6,3) forward, block variant, for layers with few channels at
 // batch > 1: input transform, the 64 Winograd-domain MFMA products and the
-// output transform in one launch, with V in registers and M in LDS.
+// output transform in one launch: V and M stay in LDS, the products'
+// accumulators in registers.
 //
 // The reference's fused kernel (/root/reference/csrc/nova_winograd_fused.hip:
 // 283-440) stages V for 16 tiles in LDS, multiplies with 16x16x16 MFMA and
