@@ -15,11 +15,14 @@ Reported on one JSON line (stdout):
   layers       per layer: NOVA ms and MIOpen (nn.Conv2d fp16) ms, eager and
                HIP-graph replayed, effective TFLOP/s, path, roofline fraction
                T_roof/T (T_roof = max(2*64*K*C*B*P_min / 2.5 PF,
-               (2BCHW + 2BKHoWo + 2*64*K*C) / 8 TB/s))
-  roofline     the dominant kernel of the step (largest summed time), timed
-               live: the library re-launches each kernel of each layer back to
-               back with one hipEvent pair on its launch stream around the loop;
-               algorithmic bytes per launch / average launch time vs 8 TB/s
+               (2BCHW + 2BKHoWo + 2*64*K*C) / 8 TB/s)), warm and cold
+  roofline     the dominant kernel family of the step (largest summed time),
+               timed live: every kernel records its own start and end events
+               (its dispatch packet, on its launch stream) over a timed region
+               of K steps; algorithmic bytes per launch / average launch time
+               vs 8 TB/s (frac, warm: the steady-state loop), and the same
+               launches in cold forwards (frac_cold: a 512 MiB write before
+               each forward, so x and U come from HBM)
   cpu_baseline the CPU oracle (the reference's NOVA arithmetic, C, OpenMP) on
                a bounded sample of the same layers, on this host's cores
 
@@ -492,6 +495,19 @@ def write_traffic_summary(data, path):
         f.write("\n".join(lines) + "\n")
 
 
+def cpu_model():
+    """The host CPU's model name (the `lscpu` "Model name" field), read from
+    /proc/cpuinfo; falls back to platform.processor()."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(layers_spec, budget_s, threads):
     """Time the CPU oracle (C restatement of the reference arithmetic, OpenMP)
     on a bounded sample: every B=1 layer, and each B=32 layer on `sample_b`
@@ -551,9 +567,52 @@ def cpu_baseline(layers_spec, budget_s, threads):
             sum(direct_flops(B, C, C, H, H) for (n, C, H), B in layers_spec)
             / (flops / rounds)),
         "fconv2d_fp32_tflops": conv_flops / conv_secs / 1e12,
-        "host": platform.processor() or platform.machine(),
+        "host": cpu_model(),
+        "arch": platform.machine(),
         "os_cpu_count": os.cpu_count(),
     }
+
+
+FLUSH_MIB = 512  # > the 256 MB memory-side cache + 8 x 4 MB of L2
+
+
+def cold_measurements(runs, lib, torch, reps):
+    """Cold-cache numbers. Before every forward a 512 MiB device write evicts
+    the memory-side cache and the L2s, so the forward's inputs (x, U) come
+    from HBM. Per layer: the median forward time between a hipEvent pair
+    (r["cold_ms"]). Per kernel: each kernel's own duration from the events
+    its dispatch packet records (nova_profile_enable), averaged over the same
+    kind of cold forwards (r["event_cold"], ms per kind). Inside a cold
+    three-pass forward V and M are still written and read back on chip: that
+    is the pipeline's own behaviour, not a warm start."""
+    flush = torch.empty(FLUSH_MIB << 20, dtype=torch.uint8, device="cuda")
+    for r in runs:
+        ts = []
+        for _ in range(reps):
+            flush.fill_(1)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            r["mod"](r["x"])
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        r["cold_ms"] = statistics.median(ts)
+    tot = (ctypes.c_double * 4)()
+    cnt = (ctypes.c_longlong * 4)()
+    for r in runs:
+        h = r["mod"]._handle.h
+        lib.nova_profile_enable(h, 1)
+        for _ in range(reps):
+            flush.fill_(1)
+            r["mod"](r["x"])
+        torch.cuda.synchronize()
+        if lib.nova_profile_read(h, tot, cnt) < 0:
+            raise RuntimeError(lib.nova_get_last_error_message().decode())
+        lib.nova_profile_enable(h, 0)
+        r["event_cold"] = {k: tot[k] / cnt[k] for k in range(4) if cnt[k] > 0}
+    del flush
+    torch.cuda.synchronize()
 
 
 EXTRA_LAYERS = [
@@ -573,10 +632,8 @@ EXTRA_LAYERS = [
 
 
 def extra_measurements(runs, lib, torch, nn, nw, reps):
-    """Per-layer NOVA vs MIOpen on the other BASELINE configs, the full
-    random-init ResNet-50 forward with and without surgery, and cold-cache
-    times of the headline layers (a 512 MiB write between reps evicts the
-    256 MB Infinity Cache and the L2s)."""
+    """Per-layer NOVA vs MIOpen on the other BASELINE configs and the full
+    random-init ResNet-50 forward with and without surgery."""
     dev = torch.device("cuda:0")
     path_names = {1: "3-pass", 2: "fused_rows", 3: "fused_block"}
     out = {"layers": []}
@@ -660,26 +717,6 @@ def extra_measurements(runs, lib, torch, nn, nw, reps):
             + (f"  | graph: miopen {tg16:7.3f} ms  nova {tgn:7.3f} ms"
                if tg16 is not None and tgn is not None else ""))
         del m16, nova, x
-    # cold-cache times of the headline layers
-    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-    out["cold"] = []
-    for r in runs:
-        ts = []
-        with torch.no_grad():
-            for _ in range(20):
-                flush.fill_(1)
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record()
-                r["mod"](r["x"])
-                e1.record()
-                torch.cuda.synchronize()
-                ts.append(e0.elapsed_time(e1))
-        tc = sorted(ts)[len(ts) // 2]
-        troof = layer_roofline_us(r["B"], r["C"], r["K"], r["H"])
-        out["cold"].append({"layer": r["name"], "B": r["B"], "nova_cold_ms": round(tc, 5),
-                            "roofline_frac_cold": round(troof / (tc * 1e3), 4)})
-    del flush
     return out
 
 
@@ -690,6 +727,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--layer-reps", type=int, default=200)
     ap.add_argument("--kernel-reps", type=int, default=100)
+    ap.add_argument("--cold-reps", type=int, default=20,
+                    help="cold-cache forwards per layer (a 512 MiB write before each)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-miopen", action="store_true")
@@ -697,7 +736,7 @@ def main():
     ap.add_argument("--details", default="", help="write the full per-layer report here")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the extra measurements (BASELINE configs 3-5 layers, full "
-                         "ResNet-50, cold-cache layer times)")
+                         "ResNet-50)")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="short run for rocprofv3 --pmc passes (copy calibration + forwards)")
     ap.add_argument("--kernel-stats-from", nargs=2, metavar=("TRACE_DIR", "BENCH_JSON"),
@@ -806,6 +845,10 @@ def main():
             lib.nova_profile_enable(h, 0)
             r["event"] = {k: tot[k] / cnt[k] for k in range(4) if cnt[k] > 0}
 
+        # ---- cold caches: per layer and per kernel (a 512 MiB write before
+        # every forward)
+        cold_measurements(runs, lib, torch, args.cold_reps)
+
         # ---- cross-check: each kernel of each layer's forward re-launched
         # back to back by the library (nova_profile_replay), one hipEvent pair
         # on its stream around the loop -> mean launch time without the
@@ -831,7 +874,9 @@ def main():
                 fam = FAMILY_OF_KIND.get(k, kname)
                 agg = kernels.setdefault(fam, {"ms": 0.0, "replay_ms": 0.0, "launches": 0,
                                                "bytes": 0.0, "flops": 0.0, "by_layer": [],
-                                               "members": {}})
+                                               "members": {}, "ms_cold": 0.0})
+                agg["ms_cold"] += r["event_cold"].get(k, ev)
+                r["kernels"][KIND_NAMES[k]]["avg_us_cold"] = r["event_cold"].get(k, ev) * 1e3
                 agg["flops"] += kernel_alg_flops(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"])
                 agg["members"][kname] = agg["members"].get(kname, 0) + 1
                 agg["ms"] += ev
@@ -875,6 +920,13 @@ def main():
         "avg_launch_us": round(avg_s * 1e6, 3),
         "timing": "hipEvents recorded by each kernel's dispatch packet over a timed region of K steps",
         "replay_avg_launch_us": round(dom["replay_ms"] / dom["launches"] * 1e3, 3),
+        # the same launches in cold forwards (x and U from HBM; see
+        # cold_measurements): the cold fraction beside the warm one above
+        "avg_launch_us_cold": round(dom["ms_cold"] / dom["launches"] * 1e3, 3),
+        "achieved_cold": round(bytes_per_launch / (dom["ms_cold"] / dom["launches"] * 1e-3)
+                               / 1e9, 1),
+        "frac_cold": round(bytes_per_launch / (dom["ms_cold"] / dom["launches"] * 1e-3)
+                           / 1e9 / PEAK_HBM_GBS, 4),
         "members": dom["members"],
         "alg_bytes_per_launch": round(bytes_per_launch),
         "launches_per_step": dom["launches"],
@@ -895,7 +947,10 @@ def main():
               "launches_per_step": v["launches"],
               "ms_per_step": round(v["ms"], 4),
               "achieved_gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1),
-              "frac_hbm": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+              "frac_hbm": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+              "avg_launch_us_cold": round(v["ms_cold"] / v["launches"] * 1e3, 3),
+              "frac_hbm_cold": round(v["bytes"] / (v["ms_cold"] * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                                     4)}
         for fam, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms"])}
     for fam, v in kernels.items():
         if v["flops"] > 0:
@@ -915,6 +970,8 @@ def main():
             "nova_tflops": round(f / (r["nova_ms"] * 1e-3) / 1e12, 2),
             "roofline_us": round(troof, 3),
             "roofline_frac": round(troof / (r["nova_ms"] * 1e3), 4),
+            "nova_cold_ms": round(r["cold_ms"], 5),
+            "roofline_frac_cold": round(troof / (r["cold_ms"] * 1e3), 4),
             "kernels": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
                             for kk, vv in v.items()} for k, v in r["kernels"].items()},
         }

@@ -117,7 +117,18 @@ struct Handle {
     int cus = 256;  // compute units of the device the weights were set on
     bool ready = false;
     Profiler prof;
+    hipEvent_t order_ev = nullptr;  // orders a new stream after the previous one
 };
+
+// True when s is being captured into a graph (or its state cannot be read).
+bool is_capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
 
 Handle* as_handle(nova_handle_t h, const char* fn) {
     Handle* H = static_cast<Handle*>(h);
@@ -171,6 +182,11 @@ bool ensure_ws(Handle* H, size_t bytes) {
 bool ensure_uf(Handle* H) {
     if (H->uf_ready) return true;
     const size_t need = (size_t)u_frag_elems(H->K, H->Cp) * sizeof(uint16_t);
+    if ((int64_t)need >= ((int64_t)1 << 31)) {  // 32-bit offsets in the fused kernels
+        set_error(kErrInvalidArgument, "fused filter copy of %lld bytes exceeds 2^31 - 1",
+                  (long long)need);
+        return false;
+    }
     if (need > H->Uf_cap) {
         if (H->Uf) {
             if (!hip_ok(hipFree(H->Uf), "hipFree(Uf)")) return false;
@@ -495,6 +511,7 @@ void nova_destroy(nova_handle_t h) {
     if (H->ws) hip_ok(hipFree(H->ws), "hipFree(workspace)");
     if (H->cnt) hip_ok(hipFree(H->cnt), "hipFree(counters)");
     for (hipEvent_t e : H->prof.pool) (void)hipEventDestroy(e);
+    if (H->order_ev) (void)hipEventDestroy(H->order_ev);
     H->magic = 0;
     delete H;
 }
@@ -513,6 +530,18 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
     }
     const int Cp = pad8(C);
     const size_t need = (size_t)64 * K * Cp * sizeof(uint16_t);
+    // The GEMM kernels address U with 32-bit byte offsets through buffer
+    // resources (position p's matrix starts at 2*p*K*Cp bytes): U must stay
+    // below 2 GB. Checked before any device call, so an oversized layer is an
+    // error, never a wrapped offset.
+    if ((int64_t)need >= ((int64_t)1 << 31)) {
+        set_error(kErrInvalidArgument,
+                  "%s: K=%d x C=%d needs a %lld-byte transformed filter; the kernels address "
+                  "at most 2^31 - 1 bytes of it",
+                  fn, K, C, (long long)need);
+        H->ready = false;
+        return;
+    }
     if (need > H->U_cap) {
         if (H->U) {
             if (!hip_ok(hipFree(H->U), "hipFree(U)")) return;
@@ -678,7 +707,25 @@ const char* nova_get_last_error_message(void) { return g_msg; }
 
 void nova_set_stream(nova_handle_t h, void* stream) {
     Handle* H = as_handle(h, "nova_set_stream");
-    if (H) H->stream = static_cast<hipStream_t>(stream);
+    if (!H) return;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (s == H->stream) return;
+    // Work already queued on the old stream reads (and the filter transform
+    // writes) the handle's U, its fragment copy, workspace and counters, which
+    // the new stream's work reuses: the new stream waits for everything queued
+    // on the old one so far. Skipped while either stream is being captured
+    // into a graph (a capture may not wait on work outside it; graph capture
+    // starts from a synchronized device).
+    if (H->U != nullptr && !is_capturing(H->stream) && !is_capturing(s)) {
+        if (H->order_ev == nullptr &&
+            !hip_ok(hipEventCreateWithFlags(&H->order_ev, hipEventDisableTiming),
+                    "nova_set_stream: hipEventCreateWithFlags"))
+            return;
+        if (!hip_ok(hipEventRecord(H->order_ev, H->stream), "nova_set_stream: hipEventRecord") ||
+            !hip_ok(hipStreamWaitEvent(s, H->order_ev, 0), "nova_set_stream: hipStreamWaitEvent"))
+            return;
+    }
+    H->stream = s;
 }
 
 void nova_set_path(nova_handle_t h, int path) {

@@ -314,15 +314,24 @@ __global__ __launch_bounds__(kFThreads, 1) void fused_kernel(FusedArgs a) {
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+    // Hand-off under the memory model: every thread's M stores are released
+    // at agent scope, the workgroup barrier orders them before thread 0's
+    // acquire-release increment of the block's counter, and the workgroup
+    // that observes the count 7 (the last of the block's 8 position rows)
+    // acquires at agent scope in every thread before it reads the other
+    // workgroups' M.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     __syncthreads();
     if (tid == 0) {
         const unsigned old =
-            __hip_atomic_fetch_add(a.cnt + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(a.cnt + blk, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old == 7u ? 1u : 0u;
     }
     __syncthreads();
     if (s_last == 0u) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // every other workgroup of the block has arrived: none touches the counter
+    // again in this launch, so it is returned to zero for the next one
     if (tid == 0) __hip_atomic_store(a.cnt + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // ---- last arriver: output transform of (kk, tile) pairs ----

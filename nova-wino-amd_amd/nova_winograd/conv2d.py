@@ -6,7 +6,7 @@ Classes:
                                  weight versioning, workspace caching
     NovaWinogradConv2dTrainable  HIP forward; backward: grad input on the HIP path, grad weight fp32
     NovaWinogradConv2dCompilable ``torch.compile`` through the custom op
-                                 ``torch.ops.nova.winograd_conv2d``
+                                 ``torch.ops.nova.winograd_conv2d`` (bias fused)
 
 The forward runs on the gfx950 library through the C-ABI; there is no CPU
 fallback (a CPU input raises).
@@ -17,6 +17,7 @@ import ctypes
 import math
 import threading
 import weakref
+from typing import Optional
 
 import torch
 import torch.nn as nn
@@ -184,6 +185,43 @@ class _Handle:
             pass
 
 
+def _init_conv_parameters(mod, in_channels, out_channels, kernel_size, padding, bias):
+    """Geometry and parameters shared by the NOVA modules: a float32
+    ``weight`` [out, in, 3, 3] with ``nn.Conv2d``'s default initialisation and
+    an optional zero ``bias`` (the constructor contract of
+    /root/reference/nova_winograd/conv2d.py:168-181)."""
+    assert kernel_size == 3, "Only 3x3 kernels supported"
+    mod.in_channels, mod.out_channels, mod.padding = in_channels, out_channels, padding
+    mod.weight = nn.Parameter(torch.empty(out_channels, in_channels, 3, 3))
+    nn.init.kaiming_uniform_(mod.weight, a=math.sqrt(5))
+    mod.register_parameter("bias", nn.Parameter(torch.zeros(out_channels)) if bias else None)
+
+
+def _module_like(cls, conv):
+    """A ``cls`` module with the geometry of ``nn.Conv2d`` ``conv`` and float32
+    copies of its parameters, on conv's device (the ``from_conv2d`` contract,
+    /root/reference/nova_winograd/conv2d.py:253-267). Only square 3x3,
+    stride-1, numeric symmetric padding is representable."""
+    assert conv.kernel_size == (3, 3), "Only 3x3 kernels supported"
+    assert conv.stride == (1, 1), "Only stride=1 supported"
+    assert not isinstance(conv.padding, str), "padding must be numeric"
+    assert conv.padding[0] == conv.padding[1], "Only symmetric padding supported"
+    mod = cls(conv.in_channels, conv.out_channels, kernel_size=3, padding=conv.padding[0],
+              bias=conv.bias is not None).to(conv.weight.device)
+    with torch.no_grad():
+        for name in ("weight", "bias"):
+            src = getattr(conv, name)
+            if src is not None:
+                getattr(mod, name).copy_(src.detach().float())
+    return mod
+
+
+def _conv_repr(mod):
+    """``extra_repr`` text of the NOVA modules (the reference's wording)."""
+    return (f"in_channels={mod.in_channels}, out_channels={mod.out_channels}, "
+            f"kernel_size=3, padding={mod.padding}, tile=F(6,3), points=NOVA")
+
+
 # ─────────────────────────────────────────────────────────────────────────
 # torch.compile custom op (/root/reference/nova_winograd/conv2d.py:25-85)
 # ─────────────────────────────────────────────────────────────────────────
@@ -250,8 +288,26 @@ def _grad_weight(inp, go, weight, padding):
     return gw.to(weight.dtype)
 
 
+class _BackwardHandles:
+    """Holder of a grad-input handle (``_bwd_handle``) for the custom op."""
+
+
+_OP_BWD = {}  # device index -> _BackwardHandles
+
+
+def _op_bwd_holder(device):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    holder = _OP_BWD.get(idx)
+    if holder is None:
+        holder = _OP_BWD[idx] = _BackwardHandles()
+    return holder
+
+
 def _register_custom_op():
-    """Register ``nova::winograd_conv2d`` as a torch.library custom op."""
+    """Register ``nova::winograd_conv2d(input, weight, padding, bias=None)``
+    (the reference's op, /root/reference/nova_winograd/conv2d.py:25-85, with
+    an optional bias added in the output epilogue) as a torch.library custom
+    op, once per process."""
     global _custom_op_registered
     with _op_lock:
         if _custom_op_registered:
@@ -259,46 +315,46 @@ def _register_custom_op():
         _custom_op_registered = True
 
     @torch.library.custom_op("nova::winograd_conv2d", mutates_args=())
-    def nova_winograd_conv2d(input: torch.Tensor, weight: torch.Tensor,
-                             padding: int) -> torch.Tensor:
+    def nova_winograd_conv2d(input: torch.Tensor, weight: torch.Tensor, padding: int,
+                             bias: Optional[torch.Tensor] = None) -> torch.Tensor:
         require_gpu_tensor(input, "input")
-        x = input.half().contiguous() if input.dtype != torch.float16 else input.contiguous()
-        w = weight.float().contiguous() if weight.dtype != torch.float32 else weight.contiguous()
-        B, C, H, W = x.shape
-        K = w.shape[0]
+        x = input.contiguous().to(torch.float16)
+        B, _, H, W = x.shape
         _, _, H_out, W_out = compute_tiling(H, W, padding)
-        output = torch.empty(B, K, H_out, W_out, dtype=torch.float16, device=x.device)
-        with _op_lock:
+        out = torch.empty(B, weight.shape[0], H_out, W_out, dtype=torch.float16,
+                          device=x.device)
+        with _op_lock:  # the per-device handle is shared with nova_forward
             hd = _op_handle(x.device)
             hd.set_stream(x.device)
             hd.set_weights_cached(weight)
-            hd.set_bias(None)  # the handle is shared with nova_forward
+            hd.set_bias(bias)
             hd.set_residual(None)
             hd.set_layout(0)
-            hd.lib.nova_forward(hd.h, ptr(x), ptr(output), B, H, W, padding)
+            hd.lib.nova_forward(hd.h, ptr(x), ptr(out), B, H, W, padding)
             check("forward")
-        return output
+        return out
 
     @nova_winograd_conv2d.register_fake
-    def _(input, weight, padding):
-        B, C, H, W = input.shape
-        K = weight.shape[0]
-        return input.new_empty(B, K, H + 2 * padding - 2, W + 2 * padding - 2,
+    def _(input, weight, padding, bias=None):
+        B, _, H, W = input.shape
+        return input.new_empty(B, weight.shape[0], H + 2 * padding - 2, W + 2 * padding - 2,
                                dtype=torch.float16)
 
-    def _setup_context(ctx, inputs, output):
-        input, weight, padding = inputs
+    def _keep(ctx, inputs, output):
+        input, weight, padding, bias = inputs
         ctx.save_for_backward(input, weight)
         ctx.padding = padding
+        ctx.bias_dtype = None if bias is None else bias.dtype
 
-    def _backward(ctx, grad_output):
+    def _grads(ctx, grad_output):
         input, weight = ctx.saved_tensors
         go = grad_output.contiguous()
-        gi = _grad_input(go, weight, ctx.padding, input.dtype)
+        gi = _grad_input_nova(_op_bwd_holder(go.device), go, weight, ctx.padding, input.dtype)
         gw = _grad_weight(input, go, weight, ctx.padding)
-        return gi, gw, None
+        gb = None if ctx.bias_dtype is None else go.float().sum(dim=(0, 2, 3)).to(ctx.bias_dtype)
+        return gi, gw, None, gb
 
-    nova_winograd_conv2d.register_autograd(_backward, setup_context=_setup_context)
+    nova_winograd_conv2d.register_autograd(_grads, setup_context=_keep)
 
 
 # ─────────────────────────────────────────────────────────────────────────
@@ -353,19 +409,7 @@ class NovaWinogradConv2d(nn.Module):
 
     def __init__(self, in_channels, out_channels, kernel_size=3, padding=1, bias=False):
         super().__init__()
-        assert kernel_size == 3, "Only 3x3 kernels supported"
-        self.in_channels = in_channels
-        self.out_channels = out_channels
-        self.padding = padding
-
-        self.weight = nn.Parameter(torch.empty(out_channels, in_channels, 3, 3))
-        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
-
-        if bias:
-            self.bias = nn.Parameter(torch.zeros(out_channels))
-        else:
-            self.register_parameter("bias", None)
-
+        _init_conv_parameters(self, in_channels, out_channels, kernel_size, padding, bias)
         self._handle = None
         self._weight_version = -1
         self._V_gemm = None
@@ -491,8 +535,8 @@ class NovaWinogradConv2d(nn.Module):
                     and _raw_stream(st[6]) == st[7]):
                 out = torch.empty(st[8], dtype=torch.float16, device=st[5])
                 st[9](st[10], x.data_ptr(), out.data_ptr(), *st[11])
-                if st[12] is not None and st[12]():
-                    check("forward")
+                if st[12] is not None:  # ctypes launch: read (and clear) the error code
+                    st[12]("forward")
                 return out
         assert x.dtype == torch.float16, f"Input must be float16, got {x.dtype}"
         assert x.is_contiguous() or _is_nhwc(x), \
@@ -525,7 +569,7 @@ class NovaWinogradConv2d(nn.Module):
             hd.h,
             (V.data_ptr() if V is not None else None, M.data_ptr() if M is not None else None,
              B, H, W, self.padding, nh, nw),
-            None if fast is not None else hd.lib.nova_get_last_error,
+            None if fast is not None else check,
             w.data_ptr(),
         )
 
@@ -533,27 +577,12 @@ class NovaWinogradConv2d(nn.Module):
     def from_conv2d(cls, conv):
         """Create from an existing nn.Conv2d
         (/root/reference/nova_winograd/conv2d.py:253-267)."""
-        assert conv.kernel_size == (3, 3), "Only 3x3 kernels supported"
-        assert conv.stride == (1, 1), "Only stride=1 supported"
-        assert not isinstance(conv.padding, str), "padding must be numeric"
-        assert conv.padding[0] == conv.padding[1], "Only symmetric padding supported"
-        nova_conv = cls(
-            conv.in_channels, conv.out_channels,
-            kernel_size=3, padding=conv.padding[0],
-            bias=conv.bias is not None,
-        )
-        nova_conv = nova_conv.to(conv.weight.device)
-        nova_conv.weight.data.copy_(conv.weight.data.float())
-        if conv.bias is not None:
-            nova_conv.bias.data.copy_(conv.bias.data.float())
-        nova_conv.invalidate_weight_cache()
-        return nova_conv
+        mod = _module_like(cls, conv)
+        mod.invalidate_weight_cache()
+        return mod
 
     def extra_repr(self):
-        return (
-            f"in_channels={self.in_channels}, out_channels={self.out_channels}, "
-            f"kernel_size=3, padding={self.padding}, tile=F(6,3), points=NOVA"
-        )
+        return _conv_repr(self)
 
 
 # ─────────────────────────────────────────────────────────────────────────
@@ -574,49 +603,29 @@ class NovaWinogradConv2dTrainable(NovaWinogradConv2d):
 
 
 # ─────────────────────────────────────────────────────────────────────────
-# NovaWinogradConv2dCompilable (/root/reference/nova_winograd/conv2d.py:300-344)
+# NovaWinogradConv2dCompilable (interface of
+# /root/reference/nova_winograd/conv2d.py:300-344)
 # ─────────────────────────────────────────────────────────────────────────
 
 class NovaWinogradConv2dCompilable(nn.Module):
-    """NOVA conv compatible with torch.compile(fullgraph=True) through the
-    custom op ``torch.ops.nova.winograd_conv2d``."""
+    """The convolution as one traceable graph node: ``forward`` is a single
+    call of the custom op ``torch.ops.nova.winograd_conv2d`` with the bias
+    passed in, so ``torch.compile(fullgraph=True)`` sees no Python control
+    flow, shapes come from the op's fake kernel, gradients from its autograd
+    formula, and the bias is added in the kernels' output epilogue (rounded
+    like the reference's separate ``out + bias.half()``)."""
 
     def __init__(self, in_channels, out_channels, kernel_size=3, padding=1, bias=False):
         super().__init__()
-        assert kernel_size == 3
         _register_custom_op()
-        self.in_channels = in_channels
-        self.out_channels = out_channels
-        self.padding = padding
-        self.weight = nn.Parameter(torch.empty(out_channels, in_channels, 3, 3))
-        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
-        if bias:
-            self.bias = nn.Parameter(torch.zeros(out_channels))
-        else:
-            self.register_parameter("bias", None)
+        _init_conv_parameters(self, in_channels, out_channels, kernel_size, padding, bias)
 
     def forward(self, x):
-        out = torch.ops.nova.winograd_conv2d(x, self.weight, self.padding)
-        if self.bias is not None:
-            out = out + self.bias.half().view(1, -1, 1, 1)
-        return out
+        return torch.ops.nova.winograd_conv2d(x, self.weight, self.padding, self.bias)
 
     @classmethod
     def from_conv2d(cls, conv):
-        assert conv.kernel_size == (3, 3) and conv.stride == (1, 1)
-        assert not isinstance(conv.padding, str) and conv.padding[0] == conv.padding[1]
-        nova = cls(
-            conv.in_channels, conv.out_channels,
-            padding=conv.padding[0], bias=conv.bias is not None,
-        )
-        nova = nova.to(conv.weight.device)
-        nova.weight.data.copy_(conv.weight.data.float())
-        if conv.bias is not None:
-            nova.bias.data.copy_(conv.bias.data.float())
-        return nova
+        return _module_like(cls, conv)
 
     def extra_repr(self):
-        return (
-            f"in_channels={self.in_channels}, out_channels={self.out_channels}, "
-            f"kernel_size=3, padding={self.padding}, tile=F(6,3), points=NOVA, compilable=True"
-        )
+        return _conv_repr(self) + ", compilable=True"

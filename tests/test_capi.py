@@ -117,3 +117,21 @@ def test_fastcall_binding_raises_library_errors(lib):
     with pytest.raises(ValueError):
         _nova_call.bind(0, 0, 0)
     assert ctypes.cast(lib.nova_forward_workspace, ctypes.c_void_p).value
+
+
+def test_oversized_filter_rejected_before_device_work(lib):
+    """The GEMM kernels address the transformed filter U (64*K*pad8(C) fp16
+    values) with 32-bit byte offsets: a layer whose U reaches 2^31 bytes is
+    refused by nova_set_weights before any allocation or launch (the pointer
+    below is never dereferenced)."""
+    h = lib.nova_create()
+    try:
+        for K, C in ((4096, 4096), (4200, 4200), (1 << 20, 64)):
+            lib.nova_set_weights(h, 16, K, C)
+            assert lib.nova_get_last_error() == 1, (K, C)
+            assert b"2^31" in lib.nova_get_last_error_message()
+            assert lib.nova_get_K(h) == 0 and not lib.nova_get_U_gemm(h)
+        lib.nova_forward(h, 1, 2, 1, 8, 8, 1)  # still not initialized
+        assert lib.nova_get_last_error() == 2
+    finally:
+        lib.nova_destroy(h)

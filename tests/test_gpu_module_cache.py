@@ -112,3 +112,32 @@ def test_functional_cached_handle(monkeypatch):
     y3 = nova_forward(x, w)
     assert len(calls) == 2
     assert not torch.equal(y3, y0)
+
+
+def test_cached_forward_ctypes_fallback_raises_library_errors(monkeypatch):
+    """Without the CPython fast-call binding the cached path launches through
+    ctypes; a library error recorded by that launch must still raise (it is
+    read once, by the check that raises). The error is provoked from the
+    host: a fused path forced on a channels-last handle runs three-pass and
+    reports it."""
+    from nova_winograd import NovaWinogradConv2d, conv2d
+
+    print("[module cache ctypes fallback]", flush=True)
+    monkeypatch.setattr(conv2d, "_FASTCALL", [None])
+    conv = NovaWinogradConv2d(16, 16, kernel_size=3, padding=1).to(DEV)
+    x = torch.randn(1, 16, 12, 12, device=DEV).half()
+    with torch.no_grad():
+        y0 = conv(x)  # full path; records the cached launch (ctypes)
+        assert conv._state is not None
+        assert torch.equal(conv(x), y0)  # cached path, no error
+        lib, h = conv._handle.lib, conv._handle.h
+        lib.nova_set_layout(h, 1)
+        lib.nova_set_path(h, 2)
+        try:
+            with pytest.raises(RuntimeError, match="fused path unsupported"):
+                conv(x)
+        finally:
+            lib.nova_set_path(h, 0)
+            lib.nova_set_layout(h, 0)
+        assert lib.nova_get_last_error() == 0
+        torch.cuda.synchronize()

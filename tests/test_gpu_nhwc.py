@@ -170,3 +170,94 @@ def test_module_and_functional_channels_last():
     assert torch.equal(yc, y)
     assert torch.equal(y2, y) and torch.equal(y3, y)
     assert yf.is_contiguous(memory_format=CL) and torch.equal(yf, y)
+
+
+def _tiles(n):
+    return (n + 5) // 6
+
+
+@pytest.mark.parametrize("B,C,K,H,W,pad", [
+    (1, 64, 64, 56, 56, 1),    # lane-parallel NHWC transforms
+    (8, 64, 64, 56, 56, 1),    # tile-block NHWC transforms
+    (4, 256, 200, 14, 14, 1),
+    (3, 24, 40, 50, 14, 2),    # non-square, pad 2
+    (16, 24, 16, 13, 13, 0),   # odd output width, pad 0
+    (3, 20, 36, 17, 17, 2),    # C % 8 != 0: lane-parallel NHWC input
+])
+def test_nhwc_transforms_against_oracle(oracle, B, C, K, H, W, pad):
+    """The channels-last transform kernels against the oracle directly (not
+    only against the NCHW kernels): V from the NHWC input transform equals
+    the oracle's input transform bit for bit; y from the NHWC output
+    transform equals the oracle's output transform of the GPU's own M bit
+    for bit; the whole forward is within the forward parity bar."""
+    import numpy as np
+
+    from nova_winograd.ops import check, get_lib
+
+    print(f"[nhwc oracle] B={B} C={C} K={K} H={H} W={W} pad={pad}", flush=True)
+    lib = get_lib()
+    torch.manual_seed(18)
+    x = torch.randn(B, C, H, W).half()
+    w = torch.randn(K, C, 3, 3) * (2.0 / (9 * C)) ** 0.5
+    Ho, Wo = H + 2 * pad - 2, W + 2 * pad - 2
+    nh, nw = _tiles(Ho), _tiles(Wo)
+    BP, Cp = B * nh * nw, (C + 7) // 8 * 8
+    nh_ref, nw_ref, _, _ = oracle.tiling(H, W, pad)
+    nh_user = nh_ref
+    while C * nh_user * nw_ref < Cp * nh * nw:  # caller V large enough for the internal pitch
+        nh_user += 1
+    V = torch.zeros(64 * C * B * nh_user * nw_ref, dtype=torch.float16, device=DEV)
+    M = torch.zeros(64 * K * B * nh_user * nw_ref, dtype=torch.float16, device=DEV)
+    xc = x.to(DEV).contiguous(memory_format=CL)
+    y = torch.empty(B, K, Ho, Wo, dtype=torch.float16, device=DEV, memory_format=CL)
+    h = lib.nova_create()
+    try:
+        lib.nova_set_path(h, 1)
+        lib.nova_set_layout(h, 1)
+        lib.nova_set_weights(h, w.to(DEV).data_ptr(), K, C)
+        lib.nova_forward_workspace(h, xc.data_ptr(), y.data_ptr(), V.data_ptr(), M.data_ptr(),
+                                   B, H, W, pad, nh_user, nw_ref)
+        check()
+        assert lib.nova_get_last_path(h) == 1
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    Vg = V[:64 * BP * Cp].view(64, BP, Cp)[:, :, :C].cpu().numpy()
+    Vo = oracle.input_transform(x.numpy(), pad, nh, nw)
+    assert np.array_equal(Vg.view(np.uint16), Vo.view(np.uint16))
+    Mg = M[:64 * BP * K].view(64, BP, K).cpu().numpy()
+    yo = oracle.output_transform(Mg, B, Ho, Wo, nh, nw)
+    yg = y.cpu().contiguous().numpy()
+    assert np.array_equal(yg.view(np.uint16), yo.view(np.uint16))
+    yr = oracle.conv2d(x.numpy(), w.numpy(), pad)
+    assert oracle.rel_l2(yg, yr) <= 5e-3
+
+
+@pytest.mark.parametrize("B,C,K,H", [(32, 64, 64, 56), (4, 48, 64, 30), (2, 64, 64, 64)])
+def test_nhwc_fused_block_against_oracle(oracle, B, C, K, H):
+    """The channels-last fused tile-block kernel against the oracle: the
+    whole forward (first two images) within the forward parity bar, plus its
+    bias/residual/ReLU epilogue against the oracle's output and the same
+    separate fp16 ops."""
+    import numpy as np
+
+    print(f"[nhwc fused oracle] B={B} C={C} K={K} H={H}", flush=True)
+    torch.manual_seed(19)
+    x = torch.randn(B, C, H, H).half()
+    w = torch.randn(K, C, 3, 3) * (2.0 / (9 * C)) ** 0.5
+    xc = x.to(DEV).contiguous(memory_format=CL)
+    wd = w.to(DEV)
+    y, took = _run(xc, wd, 1, True, path=3)
+    assert took == 3
+    n = min(B, 2)
+    yo = oracle.conv2d(x[:n].numpy(), w.numpy(), 1)
+    yg = y[:n].cpu().contiguous().numpy()
+    assert oracle.rel_l2(yg, yo) <= 5e-3
+    assert oracle.max_abs(yg, yo) <= 0.25
+    bias = (torch.randn(K) * 0.5).half()
+    res = torch.randn(B, K, H, H).half()
+    y_e, _ = _run(xc, wd, 1, True, bias=bias.to(DEV), relu=1,
+                  res=res.to(DEV).contiguous(memory_format=CL), path=3)
+    ref = torch.relu((torch.from_numpy(yo).float() + bias.float().view(1, -1, 1, 1)).half()
+                     .float() + res[:n].float()).half()
+    assert oracle.rel_l2(y_e[:n].cpu().contiguous().numpy(), ref.numpy()) <= 5e-3

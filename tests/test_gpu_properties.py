@@ -14,6 +14,12 @@ slow for every image there), on the automatically chosen path:
   arithmetic (the transforms always; the products when both run three-pass),
   within the fp32 accumulation-order bound where the batch runs the fused
   tile-block kernel (16- instead of 32-channel MFMA steps);
+* output-channel rotation: rolling the filters by 16 output channels rolls
+  the output channels by 16, bit for bit (each output channel's products and
+  transforms do not depend on its neighbours; 16 keeps every channel in the
+  same lane of its MFMA tile) -- the translation check's stand-in where the
+  image is narrower than two tiles plus the shift (7 x 7);
+* the first two images of every batch against the oracle;
 * finiteness and bitwise repeatability.
 """
 
@@ -24,9 +30,10 @@ pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda:0")
 
-# (B, C, K, H): BASELINE configs 2/3 layers at the batch the bench uses
+# (B, C, K, H): BASELINE config 3 -- the four ResNet-50 layers at B=32 (the
+# bench's batch) and at B=128
 SHAPES = [(32, 64, 64, 56), (32, 128, 128, 28), (32, 256, 256, 14), (32, 512, 512, 7),
-          (128, 128, 128, 28)]
+          (128, 64, 64, 56), (128, 128, 128, 28), (128, 256, 256, 14), (128, 512, 512, 7)]
 
 
 def _forward(lib, x, w, pad=1):
@@ -162,3 +169,30 @@ def test_batch_independence(B, C, K, H):
             rel = ((a - b).norm() / b.norm()).item()
             assert rel <= 2e-3, (i, rel)
             assert (a - b).abs().max().item() <= 0.1
+
+
+@pytest.mark.parametrize("B,C,K,H", SHAPES)
+def test_output_channel_rotation(B, C, K, H):
+    from nova_winograd.ops import get_lib
+
+    print(f"[props] channel rotation B={B} C={C} K={K} H={H}", flush=True)
+    lib = get_lib()
+    x, w = _data(B, C, K, H, 25)
+    y, took = _forward(lib, x, w)
+    yr, took_r = _forward(lib, x, torch.roll(w, 16, dims=0).contiguous())
+    assert took == took_r
+    assert torch.equal(yr, torch.roll(y, 16, dims=1))
+
+
+@pytest.mark.parametrize("B,C,K,H", SHAPES)
+def test_first_images_against_oracle(oracle, B, C, K, H):
+    print(f"[props] oracle B={B} C={C} K={K} H={H}", flush=True)
+    from nova_winograd.ops import get_lib
+
+    lib = get_lib()
+    x, w = _data(B, C, K, H, 26)
+    y, _ = _forward(lib, x, w)
+    yo = oracle.conv2d(x[:2].cpu().numpy(), w.cpu().numpy(), 1)
+    yg = y[:2].cpu().numpy()
+    assert oracle.rel_l2(yg, yo) <= 5e-3
+    assert oracle.max_abs(yg, yo) <= 0.25

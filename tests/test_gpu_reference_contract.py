@@ -1,182 +1,182 @@
-"""The reference package's own test contract, run against this package.
+"""The reference package's own acceptance contract, held against this package.
 
-Same cases, inputs and thresholds as /root/reference/tests/test_correctness.py
-(9 test functions, 25 cases): shapes + NaN/Inf, accuracy vs fp32 nn.Conv2d
-(rel-L2 < 0.06), NaN/Inf with larger weights, weight caching (bitwise repeat,
-update detection), from_conv2d, backward, surgery, a 3-step training loop and
-torch.compile(fullgraph=True) bitwise equal to eager.
+Every case, input distribution and threshold of
+/root/reference/tests/test_correctness.py (9 tests, 25 cases) is a row of
+the tables below, with the line it comes from; the checks themselves are this
+file's. Beyond the reference's bars, every forward whose inputs are known is
+also held to the CPU oracle (the same NOVA arithmetic): rel-L2 <= 5e-3.
 """
 
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from nova_winograd import (
-    NovaWinogradConv2d,
-    NovaWinogradConv2dCompilable,
-    NovaWinogradConv2dTrainable,
-    nova_forward,
-    replace_conv2d_with_nova,
-)
+import nova_winograd as nw
 
 pytestmark = pytest.mark.gpu
 
-SHAPE_CONFIGS = [  # /root/reference/tests/test_correctness.py:38-47
-    (1, 64, 64, 56, 56, 1),
-    (1, 128, 128, 28, 28, 1),
-    (1, 256, 256, 14, 14, 1),
-    (1, 512, 512, 7, 7, 1),
-    (4, 64, 64, 56, 56, 1),
-    (8, 128, 256, 28, 28, 1),
-    (1, 3, 64, 224, 224, 1),
-    (2, 64, 64, 32, 32, 1),
+DEV = "cuda"
+
+# (B, C, K, H, W, pad): output shape and no NaN/Inf (test_correctness.py:38-47)
+SHAPE_CASES = [
+    (1, 64, 64, 56, 56, 1), (1, 128, 128, 28, 28, 1), (1, 256, 256, 14, 14, 1),
+    (1, 512, 512, 7, 7, 1), (4, 64, 64, 56, 56, 1), (8, 128, 256, 28, 28, 1),
+    (1, 3, 64, 224, 224, 1), (2, 64, 64, 32, 32, 1),
 ]
-
-
-@pytest.mark.parametrize("B,C,K,H,W,pad", SHAPE_CONFIGS)
-def test_basic_shapes(B, C, K, H, W, pad):
-    print(f"[shapes] {B},{C},{K},{H},{W},{pad}", flush=True)
-    conv = NovaWinogradConv2d(C, K, kernel_size=3, padding=pad).cuda()
-    x = torch.randn(B, C, H, W, device="cuda", dtype=torch.float16)
-    out = conv(x)
-    assert out.shape == (B, K, H + 2 * pad - 2, W + 2 * pad - 2)
-    assert torch.isnan(out).sum().item() == 0
-    assert torch.isinf(out).sum().item() == 0
-
-
-ACCURACY_CONFIGS = [  # :63-69
-    ("conv2_x", 1, 64, 64, 56, 56),
-    ("conv3_x", 1, 128, 128, 28, 28),
-    ("conv4_x", 1, 256, 256, 14, 14),
-    ("conv5_x", 1, 512, 512, 7, 7),
-    ("batch8", 8, 64, 64, 56, 56),
+# (label, B, C=K, H=W): rel-L2 against fp32 nn.Conv2d (:63-69)
+ACCURACY_CASES = [
+    ("conv2_x", 1, 64, 56), ("conv3_x", 1, 128, 28), ("conv4_x", 1, 256, 14),
+    ("conv5_x", 1, 512, 7), ("batch8", 8, 64, 56),
 ]
-
-
-@pytest.mark.parametrize("name,B,C,K,H,W", ACCURACY_CONFIGS)
-def test_accuracy_vs_direct_conv(name, B, C, K, H, W):
-    print(f"[accuracy] {name}", flush=True)
-    conv_ref = nn.Conv2d(C, K, 3, padding=1, bias=False).cuda()
-    x = torch.randn(B, C, H, W, device="cuda")
-    with torch.no_grad():
-        ref = conv_ref(x)
-    out = nova_forward(x.half(), conv_ref.weight.data.float().contiguous(), padding=1)
-    rel = (torch.norm(out.float() - ref) / torch.norm(ref)).item()
-    assert rel < 0.06, f"{name}: rel_err={rel:.6f}"
-    assert torch.isnan(out).sum().item() == 0
-    assert torch.isinf(out).sum().item() == 0
-
-
-NAN_CONFIGS = [  # :89-96
-    (1, 64, 64, 56, 56),
-    (1, 128, 128, 28, 28),
-    (1, 256, 256, 14, 14),
-    (1, 512, 512, 7, 7),
-    (8, 64, 128, 56, 56),
-    (4, 256, 512, 14, 14),
+# (B, C, K, H=W): weights N(0, 0.5^2), no NaN/Inf (:89-96, :100-101)
+LARGE_WEIGHT_CASES = [
+    (1, 64, 64, 56), (1, 128, 128, 28), (1, 256, 256, 14), (1, 512, 512, 7),
+    (8, 64, 128, 56), (4, 256, 512, 14),
 ]
+REL_BAR = 0.06          # :84 and :138
+GRAD_INPUT_BAR = 0.10   # :163
+GRAD_WEIGHT_BAR = 0.15  # :164
+WEIGHT_BUMP = 0.1       # :119 (in-place update the cache must notice)
+ORACLE_BAR = 5e-3       # this build: same arithmetic, GEMM summation order only
 
 
-@pytest.mark.parametrize("B,C,K,H,W", NAN_CONFIGS)
-def test_zero_nan_inf(B, C, K, H, W):
-    print(f"[nan] {B},{C},{K},{H},{W}", flush=True)
-    x = torch.randn(B, C, H, W, device="cuda", dtype=torch.float16)
-    w = torch.randn(K, C, 3, 3, device="cuda", dtype=torch.float32) * 0.5
-    out = nova_forward(x, w, padding=1)
-    assert torch.isnan(out).sum().item() == 0
-    assert torch.isinf(out).sum().item() == 0
+def rel(a, b):
+    a, b = a.double(), b.double()
+    return ((a - b).norm() / b.norm()).item()
 
 
-def test_weight_caching():
-    conv = NovaWinogradConv2d(64, 64, kernel_size=3, padding=1).cuda()
-    x = torch.randn(1, 64, 28, 28, device="cuda", dtype=torch.float16)
-    out1 = conv(x).clone()
-    out2 = conv(x).clone()
-    assert torch.allclose(out1, out2, atol=0)
+def finite(t):
+    return bool(torch.isfinite(t).all())
+
+
+def matches_oracle(oracle, y, x16, w, pad, bias=None):
+    """rel-L2 of GPU output y against the oracle's forward on the same fp16
+    input and weights (bias added as the reference's separate fp16 add)."""
+    ref = oracle.conv2d(x16.cpu().numpy(), w.detach().float().cpu().numpy(), pad)
+    if bias is not None:
+        ref = (ref.astype(np.float32) + bias.detach().half().float().cpu().numpy()
+               [None, :, None, None]).astype(np.float16)
+    return oracle.rel_l2(y.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("case", SHAPE_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_output_shape_and_finite(case, oracle):
+    B, C, K, H, W, pad = case
+    print(f"[contract shape] {case}", flush=True)
+    mod = nw.NovaWinogradConv2d(C, K, kernel_size=3, padding=pad).to(DEV)
+    x = torch.randn(B, C, H, W, device=DEV, dtype=torch.float16)
+    y = mod(x)
+    assert tuple(y.shape) == (B, K, H + 2 * pad - 2, W + 2 * pad - 2)
+    assert finite(y)
+    assert matches_oracle(oracle, y, x, mod.weight, pad) <= ORACLE_BAR
+
+
+@pytest.mark.parametrize("label,B,C,H", ACCURACY_CASES, ids=[c[0] for c in ACCURACY_CASES])
+def test_accuracy_against_fp32_conv(label, B, C, H, oracle):
+    print(f"[contract accuracy] {label}", flush=True)
+    conv = nn.Conv2d(C, C, 3, padding=1, bias=False).to(DEV)
+    x = torch.randn(B, C, H, H, device=DEV)
+    w = conv.weight.detach().float().contiguous()
     with torch.no_grad():
-        conv.weight.add_(0.1)
-    out3 = conv(x).clone()
-    assert not torch.allclose(out1, out3, atol=1e-3)
+        truth = conv(x)
+    y = nw.nova_forward(x.half(), w, padding=1)
+    assert finite(y)
+    err = rel(y.float(), truth)
+    assert err < REL_BAR, f"{label}: rel-L2 {err:.5f} vs fp32 conv"
+    assert matches_oracle(oracle, y, x.half(), w, 1) <= ORACLE_BAR
 
 
-def test_from_conv2d():
-    std_conv = nn.Conv2d(64, 128, 3, padding=1, bias=True).cuda()
-    nova_conv = NovaWinogradConv2d.from_conv2d(std_conv).cuda()
-    assert torch.allclose(std_conv.weight.data, nova_conv.weight.data)
-    assert torch.allclose(std_conv.bias.data, nova_conv.bias.data)
-    x = torch.randn(1, 64, 28, 28, device="cuda")
+@pytest.mark.parametrize("case", LARGE_WEIGHT_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_large_weights_stay_finite(case, oracle):
+    B, C, K, H = case
+    print(f"[contract large weights] {case}", flush=True)
+    x = torch.randn(B, C, H, H, device=DEV, dtype=torch.float16)
+    w = 0.5 * torch.randn(K, C, 3, 3, device=DEV)
+    y = nw.nova_forward(x, w, padding=1)
+    assert finite(y)
+    assert matches_oracle(oracle, y, x, w, 1) <= ORACLE_BAR
+
+
+def test_filter_cache_repeats_and_follows_updates():
+    mod = nw.NovaWinogradConv2d(64, 64, kernel_size=3, padding=1).to(DEV)
+    x = torch.randn(1, 64, 28, 28, device=DEV, dtype=torch.float16)
+    first, again = mod(x).clone(), mod(x).clone()
+    assert torch.equal(first, again), "a cached forward must repeat bit for bit"
     with torch.no_grad():
-        ref = std_conv(x)
-        out = nova_conv(x.half())
-    rel = (torch.norm(out.float() - ref) / torch.norm(ref)).item()
-    assert rel < 0.06
+        mod.weight.add_(WEIGHT_BUMP)
+    assert not torch.allclose(first, mod(x), atol=1e-3), "in-place weight update ignored"
 
 
-def test_backward_pass():
-    C, K = 32, 64
-    nova_conv = NovaWinogradConv2dTrainable(C, K, kernel_size=3, padding=1, bias=True).cuda()
-    ref_conv = nn.Conv2d(C, K, 3, padding=1, bias=True).cuda()
-    ref_conv.weight.data.copy_(nova_conv.weight.data)
-    ref_conv.bias.data.copy_(nova_conv.bias.data)
-    x = torch.randn(2, C, 14, 14, device="cuda", requires_grad=True)
-    ref_out = ref_conv(x)
-    ref_out.sum().backward()
-    ref_gi = x.grad.clone()
-    x.grad = None
-    out = nova_conv(x)
-    out.float().sum().backward()
-    gi = x.grad.clone()
-    gi_err = (torch.norm(gi - ref_gi) / torch.norm(ref_gi)).item()
-    gw_err = (torch.norm(nova_conv.weight.grad - ref_conv.weight.grad)
-              / torch.norm(ref_conv.weight.grad)).item()
-    assert gi_err < 0.10, f"grad_input rel_err={gi_err:.6f}"
-    assert gw_err < 0.15, f"grad_weight rel_err={gw_err:.6f}"
+def test_from_conv2d_copies_and_agrees(oracle):
+    ref = nn.Conv2d(64, 128, 3, padding=1, bias=True).to(DEV)
+    mod = nw.NovaWinogradConv2d.from_conv2d(ref).to(DEV)
+    assert torch.equal(mod.weight, ref.weight) and torch.equal(mod.bias, ref.bias)
+    x = torch.randn(1, 64, 28, 28, device=DEV)
+    with torch.no_grad():
+        truth, y = ref(x), mod(x.half())
+    assert rel(y.float(), truth) < REL_BAR
+    assert matches_oracle(oracle, y, x.half(), ref.weight, 1, ref.bias) <= ORACLE_BAR
 
 
-def test_replace_conv2d():
-    model = nn.Sequential(
-        nn.Conv2d(3, 64, 3, padding=1, bias=False),
-        nn.ReLU(),
-        nn.Conv2d(64, 128, 3, stride=2, padding=1),
-        nn.ReLU(),
-        nn.Conv2d(128, 128, 3, padding=1, bias=True),
-        nn.ReLU(),
-        nn.Conv2d(128, 256, 1),
-    ).cuda()
-    n = replace_conv2d_with_nova(model, verbose=False)
-    assert n == 2
-    assert isinstance(model[0], NovaWinogradConv2d)
-    assert not isinstance(model[2], NovaWinogradConv2d)
-    assert isinstance(model[4], NovaWinogradConv2d)
-    x = torch.randn(1, 3, 16, 16, device="cuda", dtype=torch.float16)
-    model[0](x)  # the swapped layers run
+def _trainable_pair(C=32, K=64):
+    mod = nw.NovaWinogradConv2dTrainable(C, K, kernel_size=3, padding=1, bias=True).to(DEV)
+    ref = nn.Conv2d(C, K, 3, padding=1, bias=True).to(DEV)
+    with torch.no_grad():
+        ref.weight.copy_(mod.weight)
+        ref.bias.copy_(mod.bias)
+    return mod, ref
 
 
-def test_training_step():
-    conv = NovaWinogradConv2dTrainable(32, 64, kernel_size=3, padding=1, bias=True).cuda()
-    opt = torch.optim.SGD(conv.parameters(), lr=0.01)
-    x = torch.randn(2, 32, 14, 14, device="cuda")
-    target = torch.randn(2, 64, 14, 14, device="cuda", dtype=torch.float16)
+def test_trainable_gradients_track_fp32():
+    mod, ref = _trainable_pair()
+    x = torch.randn(2, 32, 14, 14, device=DEV, requires_grad=True)
+    ref(x).sum().backward()
+    gi_truth, x.grad = x.grad.clone(), None
+    mod(x).float().sum().backward()
+    gi_err = rel(x.grad, gi_truth)
+    gw_err = rel(mod.weight.grad, ref.weight.grad)
+    assert gi_err < GRAD_INPUT_BAR, f"grad input rel-L2 {gi_err:.5f}"
+    assert gw_err < GRAD_WEIGHT_BAR, f"grad weight rel-L2 {gw_err:.5f}"
+
+
+def test_surgery_swaps_only_eligible_layers():
+    net = nn.Sequential(
+        nn.Conv2d(3, 64, 3, padding=1, bias=False), nn.ReLU(),
+        nn.Conv2d(64, 128, 3, stride=2, padding=1), nn.ReLU(),   # stride 2: kept
+        nn.Conv2d(128, 128, 3, padding=1, bias=True), nn.ReLU(),
+        nn.Conv2d(128, 256, 1),                                   # 1x1: kept
+    ).to(DEV)
+    assert nw.replace_conv2d_with_nova(net, verbose=False) == 2
+    swapped = [isinstance(m, nw.NovaWinogradConv2d) for m in net]
+    assert swapped == [True, False, False, False, True, False, False]
+    y = net[0](torch.randn(1, 3, 16, 16, device=DEV, dtype=torch.float16))
+    assert tuple(y.shape) == (1, 64, 16, 16) and finite(y)
+
+
+def test_three_sgd_steps_reduce_loss():
+    mod, _ = _trainable_pair()
+    opt = torch.optim.SGD(mod.parameters(), lr=0.01)
+    x = torch.randn(2, 32, 14, 14, device=DEV)
+    target = torch.randn(2, 64, 14, 14, device=DEV, dtype=torch.float16)
     losses = []
     for _ in range(3):
         opt.zero_grad()
-        out = conv(x)
-        loss = F.mse_loss(out, target)
+        loss = F.mse_loss(mod(x), target)
         loss.backward()
         opt.step()
         losses.append(loss.item())
-    assert losses[-1] < losses[0], f"Loss not decreasing: {losses}"
-    assert conv.weight.grad is not None
+    assert losses[-1] < losses[0], f"loss did not fall: {losses}"
+    assert mod.weight.grad is not None
 
 
-def test_torch_compile():
-    conv = NovaWinogradConv2dCompilable(64, 128, kernel_size=3, padding=1).cuda()
-    x = torch.randn(2, 64, 28, 28, device="cuda", dtype=torch.float16)
+def test_compiled_module_equals_eager(oracle):
+    mod = nw.NovaWinogradConv2dCompilable(64, 128, kernel_size=3, padding=1).to(DEV)
+    x = torch.randn(2, 64, 28, 28, device=DEV, dtype=torch.float16)
     with torch.no_grad():
-        eager = conv(x)
-    compiled = torch.compile(conv, fullgraph=True)
-    with torch.no_grad():
-        out = compiled(x)
-    assert torch.allclose(eager, out, atol=0)
-    assert torch.isnan(out).sum().item() == 0
+        eager = mod(x)
+        compiled = torch.compile(mod, fullgraph=True)(x)
+    assert torch.equal(eager, compiled)
+    assert finite(compiled)
+    assert matches_oracle(oracle, eager, x, mod.weight, 1) <= ORACLE_BAR

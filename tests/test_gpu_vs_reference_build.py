@@ -112,9 +112,17 @@ def test_reference_output_transform(oracle, B, K, Ho):
     _near_bitexact(yo.view(np.uint16), _u16(y_ref), "y oracle vs reference")
 
 
-@pytest.mark.parametrize("B,C,K,H", [(1, 64, 64, 56), (1, 128, 128, 28), (1, 256, 256, 14),
-                                     (1, 512, 512, 7), (2, 192, 48, 14)])
+@pytest.mark.parametrize("B,C,K,H", [
+    (1, 64, 64, 56), (1, 128, 128, 28), (1, 256, 256, 14), (1, 512, 512, 7),
+    (2, 192, 48, 14),
+    # BASELINE configs 2/3 at B=32 and one SD-1.5 layer of config 4
+    (32, 64, 64, 56), (32, 128, 128, 28), (32, 256, 256, 14), (32, 512, 512, 7),
+    (2, 640, 640, 32),
+])
 def test_reference_whole_path(oracle, B, C, K, H):
+    """Whole forwards of both libraries on the same input: close to each
+    other over the whole batch, and at the same error level against the fp64
+    direct convolution (on the first images: the CPU truth is slow)."""
     print(f"[ref path] B={B} C={C} K={K} H={H}", flush=True)
     L = ref_lib()
     torch.manual_seed(0)
@@ -133,9 +141,12 @@ def test_reference_whole_path(oracle, B, C, K, H):
 
     y = nw.nova_forward(xd, wd.contiguous(), 1)
     torch.cuda.synchronize()
-    truth = oracle.direct_conv2d(x.numpy(), w.numpy(), 1)
-    yr, yg = y_ref.cpu().numpy(), y.cpu().numpy()
-    yo = oracle.conv2d(x.numpy(), w.numpy(), 1)
+    n = B if B <= 2 and C * K <= 512 * 512 else (1 if C * K > 512 * 512 else 2)
+    truth = oracle.direct_conv2d(x[:n].numpy(), w.numpy(), 1)
+    yr_all, yg_all = y_ref.cpu().numpy(), y.cpu().numpy()
+    assert oracle.rel_l2(yg_all, yr_all) <= 5e-3  # the whole batch
+    yr, yg = yr_all[:n], yg_all[:n]
+    yo = oracle.conv2d(x[:n].numpy(), w.numpy(), 1)
     rel_ref, rel_gpu, rel_or = (oracle.rel_l2(a, truth) for a in (yr, yg, yo))
     print(f"rel-L2 vs fp64: reference {rel_ref:.4e}  this build {rel_gpu:.4e}  oracle {rel_or:.4e}; "
           f"build vs reference {oracle.rel_l2(yg, yr):.2e}; oracle vs reference "
