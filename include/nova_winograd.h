@@ -162,6 +162,22 @@ NOVA_API void nova_set_residual(nova_handle_t h, const void* d_residual_f16);
  * (position rows), 3 = fused (tile blocks), 4 = windowed 3-pass. */
 NOVA_API int nova_get_last_path(nova_handle_t h);
 
+/* No counterpart in the reference. nova_forward for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. Same result as nova_forward on the same
+ * handle, bit for bit, and nothing is allocated: the three-pass workspace is a
+ * scratch array of NOVA_NOALLOC_SCRATCH_BYTES compiled into the library (one
+ * copy per GPU, held until the process ends), batches are split so every
+ * launch fits it, and a shape whose single image needs more workspace than
+ * that is refused (error 4, output untouched). Every call on a GPU shares that
+ * GPU's scratch: calls that overlap on one GPU (unordered streams, other host
+ * threads) race. The position-row fused path needs allocated scratch and is
+ * never taken here (a forced path 2 runs three-pass and reports it), and these
+ * calls are not timed by nova_profile_enable. */
+#define NOVA_NOALLOC_SCRATCH_BYTES (64ll << 20)
+NOVA_API void nova_forward_noalloc(nova_handle_t h, const void* d_input, void* d_output, int batch,
+                                   int H, int W, int pad);
+
 /* Internal workspace bytes a forward of this shape needs on this handle. */
 NOVA_API long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad);
 

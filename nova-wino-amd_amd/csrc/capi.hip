@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <cstring>
 #include <functional>
+#include <mutex>
 #include <vector>
 
 #include "../../include/nova_winograd.h"
@@ -115,6 +116,7 @@ struct Handle {
     int nhwc = 0;       // 1: x and y are NHWC (channels last)
     int last_path = 0;
     int cus = 256;  // compute units of the device the weights were set on
+    int device = 0;  // that device
     bool ready = false;
     Profiler prof;
     hipEvent_t order_ev = nullptr;  // orders a new stream after the previous one
@@ -337,7 +339,7 @@ int choose_path(const Handle* Hd, const Shape& s) {
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
 bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* V,
-                    uint16_t* M, bool remember, const Epilogue& ep) {
+                    uint16_t* M, bool remember, const Epilogue& ep, bool timed = true) {
     Profiler& pf = Hd->prof;
     const hipStream_t st = Hd->stream;
     const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
@@ -359,23 +361,65 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
         pf.last[kKindOutput] = out;
         pf.last[kKindFused] = nullptr;
     }
-    size_t e = pf.arm();
+    // timed = false (allocation-free forwards): never arm the profiler, whose
+    // event pool may grow
+    size_t e = timed ? pf.arm() : SIZE_MAX;
     const bool ok_in = hip_ok(in(), "input transform");
     pf.done(kKindInput, e, "input_transform_kernel");
     if (!ok_in) return false;
-    e = pf.arm();
+    e = timed ? pf.arm() : SIZE_MAX;
     const bool ok_gm = hip_ok(gm(), "wgemm");
     pf.done(kKindGemm, e, wgemm_name(K, Cp, (int)s.BP));
     if (!ok_gm) return false;
-    e = pf.arm();
+    e = timed ? pf.arm() : SIZE_MAX;
     const bool ok_out = hip_ok(out(), "output transform");
     pf.done(kKindOutput, e, "output_transform_kernel");
     return ok_out;
 }
 
+// ---- scratch of the allocation-free forward (nova_forward_noalloc) -------
+// The three-pass V/M workspace for callers that cannot allocate device
+// memory. One copy per GPU, in device memory the loader reserves with the
+// library's code object; it lives until the process ends. In host code the
+// name `scratch` is only a stand-in symbol, never a device address: the
+// kernels get the per-device address that hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[NOVA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on device dev, looked up once per device with
+// that device current (each GPU holds its own copy at its own address).
+void* scratch_ptr(int dev, const char* fn) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_error(kErrInvalidArgument, "%s: device %d out of range", fn, dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        int cur = 0;
+        if (!hip_ok(hipGetDevice(&cur), "hipGetDevice")) return nullptr;
+        if (cur != dev && !hip_ok(hipSetDevice(dev), "hipSetDevice")) return nullptr;
+        void* p = nullptr;
+        const bool ok = hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                               "hipGetSymbolAddress(scratch)");
+        if (cur != dev) (void)hipSetDevice(cur);
+        if (!ok || p == nullptr) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
 // Core forward. V_user/M_user may be null; caps are in fp16 elements.
+// scratch_dev != null: the allocation-free form -- the three-pass workspace is
+// that buffer (NOVA_NOALLOC_SCRATCH_BYTES), batches are split to fit it, and
+// nothing is allocated (no workspace, counters, fragment copy or profiler
+// events).
 void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* V_user,
-                  int64_t V_cap, void* M_user, int64_t M_cap, const char* fn) {
+                  int64_t V_cap, void* M_user, int64_t M_cap, const char* fn,
+                  void* scratch_dev = nullptr) {
+    const bool no_alloc = scratch_dev != nullptr;
     if (!Hd->ready) {
         set_error(kErrNotInitialized, "%s: call nova_set_weights() before forward", fn);
         return;
@@ -394,6 +438,22 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     // the channels-last tile-block kernel stages x with 16-byte loads
     if (path == 3 && Hd->nhwc && !aligned16(x)) path = 1;
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s_all));
+    if (no_alloc) {
+        // the position-row kernel needs an allocated M buffer and counters,
+        // and a fragment copy not yet built would be allocated here
+        if (path == 2 || (path == 3 && !Hd->uf_ready)) path = 1;
+        const int64_t per_img = 2 * (int64_t)64 * (Hd->Cp + Hd->K) * s_all.nh * s_all.nw;
+        if (path != 3 && per_img > (int64_t)NOVA_NOALLOC_SCRATCH_BYTES - 256) {
+            set_error(kErrWorkspace,
+                      "%s: one image needs %lld bytes of workspace; the allocation-free "
+                      "forward holds %lld",
+                      fn, (long long)per_img, (long long)NOVA_NOALLOC_SCRATCH_BYTES);
+            return;
+        }
+        // V, then M at the next 256-byte boundary
+        if (path != 3)
+            chunk = std::min<int64_t>(chunk, (NOVA_NOALLOC_SCRATCH_BYTES - 256) / per_img);
+    }
     const bool fused = path == 2 || path == 3;
     if (fused && !ensure_uf(Hd)) return;
     if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3)) {
@@ -408,7 +468,10 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     const int64_t needM = 64 * (int64_t)Hd->K * BPc;
     uint16_t* V = nullptr;
     uint16_t* M = nullptr;
-    if (!fused) {
+    if (!fused && no_alloc) {
+        V = static_cast<uint16_t*>(scratch_dev);
+        M = V + ((needV + 127) & ~(int64_t)127);  // 256-byte aligned
+    } else if (!fused) {
         size_t ws_bytes = 0;
         const bool userV = V_user && needV <= V_cap && aligned16(V_user);
         const bool userM = M_user && needM <= M_cap && aligned16(M_user);
@@ -450,11 +513,11 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 return launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
                                           s.Ho, s.Wo, bp, st, ep);
             };
-            if (b0 == 0) {
+            if (b0 == 0 && !no_alloc) {
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
                 pf.last[kKindFused] = fz;
             }
-            const size_t e0 = pf.arm();
+            const size_t e0 = no_alloc ? SIZE_MAX : pf.arm();
             const bool ok = hip_ok(fz(), "fused block kernel");
             pf.done(kKindFused, e0, "fused_block_kernel");
             if (!ok) return;
@@ -483,7 +546,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             const bool ok = hip_ok(fz(), "fused kernel");
             pf.done(kKindFused, e0, fused_name(fp));
             if (!ok) return;
-        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0, ep)) {
+        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0 && !no_alloc, ep, !no_alloc)) {
             return;
         }
     }
@@ -559,10 +622,13 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
     H->C = C;
     H->Cp = Cp;
     int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        cus > 0)
-        H->cus = cus;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        H->device = dev;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ==
+                hipSuccess &&
+            cus > 0)
+            H->cus = cus;
+    }
     H->ready = hip_ok(launch_filter_transform_gemm(d_weight, w_f16, H->U, K, C, Cp, H->stream),
                       "filter transform");
     const bool fused_possible = (C <= 64 && K <= 64 && H->path_pref == 0) ||
@@ -589,6 +655,21 @@ void nova_forward(nova_handle_t h, const void* d_input, void* d_output, int batc
     Shape s;
     if (!make_shape(Hd, batch, H, W, pad, &s, "nova_forward")) return;
     forward_impl(Hd, d_input, d_output, s, nullptr, 0, nullptr, 0, "nova_forward");
+}
+
+void nova_forward_noalloc(nova_handle_t h, const void* d_input, void* d_output, int batch, int H,
+                          int W, int pad) {
+    Handle* Hd = as_handle(h, "nova_forward_noalloc");
+    if (!Hd) return;
+    Shape s;
+    if (!make_shape(Hd, batch, H, W, pad, &s, "nova_forward_noalloc")) return;
+    if (!Hd->ready) {
+        set_error(kErrNotInitialized, "nova_forward_noalloc: call nova_set_weights() before forward");
+        return;
+    }
+    void* scr = scratch_ptr(Hd->device, "nova_forward_noalloc");
+    if (scr == nullptr) return;
+    forward_impl(Hd, d_input, d_output, s, nullptr, 0, nullptr, 0, "nova_forward_noalloc", scr);
 }
 
 void nova_forward_workspace(nova_handle_t h, const void* d_input, void* d_output,
