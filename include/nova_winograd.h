@@ -115,6 +115,18 @@ NOVA_API const char* nova_get_last_error_message(void);
  * for bit. */
 NOVA_API void nova_set_weights_f16(nova_handle_t h, const void* d_weight_f16, int K, int C);
 
+/* No counterpart in the reference's C-ABI: the weight gradient, which the
+ * reference computes in fp32 PyTorch with a per-sample unfold loop
+ * (/root/reference/nova_winograd/conv2d.py:121-147). d_grad_weight receives
+ * fp32 dL/dw [K][C][3][3] (overwritten) for x fp16 [B][C][H][W] and
+ * d_grad_output [B][K][Ho][Wo] (fp16, or fp32 when grad_f32 = 1), NCHW,
+ * padding pad. Computed on the Winograd domain in fp32 (the products reduced
+ * over the tiles, deterministic), on the handle's stream with the handle's
+ * workspace; the handle needs no weights. batch = 0 writes zeros. */
+NOVA_API void nova_weight_grad(nova_handle_t h, const void* d_input, const void* d_grad_output,
+                               void* d_grad_weight, int batch, int C, int K, int H, int W,
+                               int pad, int grad_f32);
+
 /* Stream for the handle's subsequent work (a hipStream_t; NULL = null stream). */
 NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
 

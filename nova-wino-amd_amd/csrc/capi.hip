@@ -690,6 +690,35 @@ void nova_forward_workspace(nova_handle_t h, const void* d_input, void* d_output
                  64 * (int64_t)Hd->K * bp_user, "nova_forward_workspace");
 }
 
+void nova_weight_grad(nova_handle_t h, const void* d_input, const void* d_grad_output,
+                      void* d_grad_weight, int batch, int C, int K, int H, int W, int pad,
+                      int grad_f32) {
+    Handle* Hd = as_handle(h, "nova_weight_grad");
+    if (!Hd) return;
+    if (d_grad_weight == nullptr || batch < 0 || C < 1 || K < 1 || H < 1 || W < 1 || pad < 0 ||
+        (grad_f32 != 0 && grad_f32 != 1) || H + 2 * pad - 2 < 1 || W + 2 * pad - 2 < 1 ||
+        (batch > 0 && (d_input == nullptr || d_grad_output == nullptr))) {
+        set_error(kErrInvalidArgument, "nova_weight_grad: bad arguments");
+        return;
+    }
+    int dev = 0, cus = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1)
+        cus = 256;
+    const WgradPlan pl = wgrad_plan(batch, C, K, H, W, pad, cus);
+    if (!pl.ok) {
+        set_error(kErrInvalidArgument,
+                  "nova_weight_grad: one image of this shape exceeds the kernels' 32-bit offsets");
+        return;
+    }
+    if (!ensure_ws(Hd, (size_t)pl.ws_bytes)) return;
+    hip_ok(launch_wgrad(static_cast<const uint16_t*>(d_input), d_grad_output, grad_f32 != 0,
+                        static_cast<float*>(d_grad_weight), batch, C, K, H, W, pad, pl, Hd->ws,
+                        Hd->stream),
+           "weight gradient");
+}
+
 void nova_compute_tiling(int H, int W, int pad, int* nh, int* nw, int* H_out, int* W_out) {
     if (!nh || !nw || !H_out || !W_out) {
         set_error(kErrInvalidArgument, "nova_compute_tiling: null output pointer");

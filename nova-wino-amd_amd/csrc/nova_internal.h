@@ -149,4 +149,24 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
                               int Wo, const FusedBlockPlan& p, hipStream_t s,
                               Epilogue ep = Epilogue());
 
+// ---- weight gradient (Winograd domain, fp32) --------------------------------
+// Plan of a weight-gradient computation: images per sub-batch (the fp32
+// transformed operands stay below 2^31 bytes each and 1 GiB together), the
+// padded tile count of the largest sub-batch, the number of splits of the
+// tile range in the products, the workspace it needs, and whether the shape
+// fits the kernels' 32-bit offsets at all.
+struct WgradPlan {
+    int chunk_images;
+    int nsplit;  // partial filters: ranges of the tile index
+    int64_t BPp_max;
+    int64_t ws_bytes;
+    bool ok;
+};
+WgradPlan wgrad_plan(int B, int C, int K, int H, int W, int pad, int cus);
+// dw[K][C][3][3] (fp32, overwritten) for x fp16 [B][C][H][W] and dY
+// [B][K][Ho][Wo] (fp16, or fp32 if dy_f32); ws holds plan.ws_bytes.
+hipError_t launch_wgrad(const uint16_t* x, const void* dy, bool dy_f32, float* dw, int B, int C,
+                        int K, int H, int W, int pad, const WgradPlan& plan, void* ws,
+                        hipStream_t s);
+
 }  // namespace nova

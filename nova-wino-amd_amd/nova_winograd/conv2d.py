@@ -4,7 +4,8 @@
 Classes:
     NovaWinogradConv2d           inference module: cached filter transform,
                                  weight versioning, workspace caching
-    NovaWinogradConv2dTrainable  HIP forward; backward: grad input on the HIP path, grad weight fp32
+    NovaWinogradConv2dTrainable  HIP forward and backward (grad input through the
+                                 forward kernels, grad weight on the Winograd domain)
     NovaWinogradConv2dCompilable ``torch.compile`` through the custom op
                                  ``torch.ops.nova.winograd_conv2d`` (bias fused)
 
@@ -257,10 +258,7 @@ def _grad_input_nova(holder, go, weight, padding, dtype):
     pb = 2 - padding
     if pb < 0:
         return _grad_input(go, weight, padding, dtype)
-    hd = getattr(holder, "_bwd_handle", None)
-    if hd is None:
-        hd = _Handle()
-        holder._bwd_handle = hd
+    hd = _bwd_handle(holder)
     hd.set_stream(go.device)
     # the flipped filter is cached for this exact weight tensor (weak
     # reference: a freed tensor whose memory is reused can never match) at
@@ -280,11 +278,38 @@ def _grad_input_nova(holder, go, weight, padding, dtype):
     return gi.to(dtype)
 
 
-def _grad_weight(inp, go, weight, padding):
-    # One batched fp32 correlation instead of the reference's per-sample
-    # unfold loop (/root/reference/nova_winograd/conv2d.py:138-143).
-    gw = torch.nn.grad.conv2d_weight(inp.float(), tuple(weight.shape), go.float(),
-                                     padding=padding)
+def _bwd_handle(holder):
+    """The handle a module (or the custom op's per-device holder) uses for
+    its backward kernels: the flipped filter of grad input, and the
+    workspace and stream of grad weight."""
+    hd = getattr(holder, "_bwd_handle", None)
+    if hd is None:
+        hd = _Handle()
+        holder._bwd_handle = hd
+    return hd
+
+
+def _grad_weight(holder, inp, go, weight, padding):
+    """dL/dw on the HIP path (nova_weight_grad): the Winograd-domain
+    products of the transformed input and the transformed output gradient,
+    reduced over the tiles and mapped back through G, all in fp32 -- in place
+    of the reference's per-sample fp32 unfold loop
+    (/root/reference/nova_winograd/conv2d.py:121-147). The input is the fp16
+    tensor the forward convolved, so this is the gradient of the forward as
+    computed."""
+    hd = _bwd_handle(holder)
+    hd.set_stream(go.device)
+    x16 = inp.detach().to(torch.float16).contiguous()
+    g = go.detach()
+    if g.dtype not in (torch.float16, torch.float32):
+        g = g.float()
+    g = g.contiguous()
+    B, C, H, W = x16.shape
+    K = weight.shape[0]
+    gw = torch.empty(K, C, 3, 3, dtype=torch.float32, device=go.device)
+    hd.lib.nova_weight_grad(hd.h, ptr(x16), ptr(g), ptr(gw), B, C, K, H, W, padding,
+                            1 if g.dtype == torch.float32 else 0)
+    check("backward (grad weight)")
     return gw.to(weight.dtype)
 
 
@@ -350,7 +375,7 @@ def _register_custom_op():
         input, weight = ctx.saved_tensors
         go = grad_output.contiguous()
         gi = _grad_input_nova(_op_bwd_holder(go.device), go, weight, ctx.padding, input.dtype)
-        gw = _grad_weight(input, go, weight, ctx.padding)
+        gw = _grad_weight(_op_bwd_holder(go.device), input, go, weight, ctx.padding)
         gb = None if ctx.bias_dtype is None else go.float().sum(dim=(0, 2, 3)).to(ctx.bias_dtype)
         return gi, gw, None, gb
 
@@ -363,7 +388,8 @@ def _register_custom_op():
 
 class NovaWinogradFunction(torch.autograd.Function):
     """HIP forward; backward: grad input through the HIP forward (flipped
-    filter), grad weight and bias in fp32."""
+    filter), grad weight through nova_weight_grad (fp32, Winograd domain),
+    grad bias a channel sum."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, padding, handle_holder):
@@ -382,7 +408,7 @@ class NovaWinogradFunction(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             grad_input = _grad_input_nova(ctx.holder, go, weight, padding, input.dtype)
         if ctx.needs_input_grad[1]:
-            grad_weight = _grad_weight(input, go, weight, padding)
+            grad_weight = _grad_weight(ctx.holder, input, go, weight, padding)
         if bias is not None and ctx.needs_input_grad[2]:
             grad_bias = go.float().sum(dim=(0, 2, 3)).to(bias.dtype)
         return grad_input, grad_weight, grad_bias, None, None
@@ -590,7 +616,7 @@ class NovaWinogradConv2d(nn.Module):
 # ─────────────────────────────────────────────────────────────────────────
 
 class NovaWinogradConv2dTrainable(NovaWinogradConv2d):
-    """NOVA conv with backward support: HIP forward and grad input, fp32 grad
+    """NOVA conv with backward support: HIP forward, grad input and grad
     weight."""
 
     def forward(self, x):

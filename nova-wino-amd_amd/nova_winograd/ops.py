@@ -61,6 +61,7 @@ _SIGNATURES = {
     "nova_get_last_path": (_i, [_vp]),
     "nova_workspace_bytes": (ctypes.c_longlong, [_vp, _i, _i, _i, _i]),
     "nova_forward_noalloc": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "nova_weight_grad": (None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i]),
     "nova_profile_enable": (None, [_vp, _i]),
     "nova_profile_read": (_i, [_vp, ctypes.POINTER(ctypes.c_double),
                                ctypes.POINTER(ctypes.c_longlong)]),

@@ -427,3 +427,38 @@ void nvo_direct(const uint16_t* x, const float* w, int B, int C, int K, int H, i
         y[idx] = s;
     }
 }
+
+/*
+ * Weight gradient of the 3x3 correlation (truth for the GPU's Winograd-domain
+ * gradient), accumulated in double:
+ *   gw[k][c][a][b] = sum_{n,oh,ow} dy[n][k][oh][ow] * x[n][c][oh-pad+a][ow-pad+b]
+ * (x outside the image is zero). This is the gradient the reference computes
+ * in fp32 with its per-sample unfold loop
+ * (/root/reference/nova_winograd/conv2d.py:121-147); dy is fp32 here.
+ */
+void nvo_weight_grad(const uint16_t* x, const float* dy, int B, int C, int K, int H, int W,
+                     int pad, double* gw) {
+    int Ho = H + 2 * pad - 2, Wo = W + 2 * pad - 2;
+    long total = (long)K * C * 9;
+#pragma omp parallel for schedule(static)
+    for (long idx = 0; idx < total; idx++) {
+        int fb = (int)(idx % 3);
+        int fa = (int)((idx / 3) % 3);
+        int c = (int)((idx / 9) % C);
+        int k = (int)(idx / (9L * C));
+        double s = 0.0;
+        for (int n = 0; n < B; n++)
+            for (int oh = 0; oh < Ho; oh++) {
+                int ih = oh - pad + fa;
+                if (ih < 0 || ih >= H) continue;
+                const float* g = dy + (((long)n * K + k) * Ho + oh) * Wo;
+                const uint16_t* xr = x + (((long)n * C + c) * H + ih) * W;
+                for (int ow = 0; ow < Wo; ow++) {
+                    int iw = ow - pad + fb;
+                    if (iw < 0 || iw >= W) continue;
+                    s += (double)g[ow] * (double)f16_to_f32(xr[iw]);
+                }
+            }
+        gw[idx] = s;
+    }
+}

@@ -63,6 +63,7 @@ def lib():
     L.nvo_conv.argtypes = [_u16p, _f32p] + [_c_int] * 6 + [_u16p]
     L.nvo_conv.restype = _c_int
     L.nvo_direct.argtypes = [_u16p, _f32p] + [_c_int] * 6 + [_f64p]
+    L.nvo_weight_grad.argtypes = [_u16p, _f32p] + [_c_int] * 6 + [_f64p]
     _lib = L
     return L
 
@@ -182,6 +183,19 @@ def direct_conv2d(x, w, pad=1):
     y = np.empty((B, K, Ho, Wo), np.float64)
     lib().nvo_direct(xb.reshape(-1), w.reshape(-1), B, C, K, H, W, pad, y.reshape(-1))
     return y
+
+
+def weight_grad(x, dy, pad=1):
+    """Truth for the weight gradient: fp64 accumulation of
+    dy[n,k,oh,ow] * x[n,c,oh-pad+a,ow-pad+b] for fp16 x [B,C,H,W] and fp32 dy
+    [B,K,Ho,Wo]; returns fp64 [K,C,3,3]."""
+    xb = _h(x)
+    dy = _f32(dy)
+    B, C, H, W = x.shape
+    K = dy.shape[1]
+    gw = np.empty((K, C, 3, 3), np.float64)
+    lib().nvo_weight_grad(xb.reshape(-1), dy.reshape(-1), B, C, K, H, W, pad, gw.reshape(-1))
+    return gw
 
 
 def rel_l2(a, b):

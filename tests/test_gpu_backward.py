@@ -125,3 +125,119 @@ def test_grad_input_follows_weight_updates():
     conv.invalidate_weight_cache()
     g3 = grad_input(conv)
     assert torch.equal(g3, grad_input(fresh())) and not torch.equal(g3, g2)
+
+
+# (B, C, K, H, W, pad): edge tiles, K and C off the 64-blocks, pads 0-2,
+# non-square, the ResNet-50 layers at B=1 and B=32 and one multi-sub-batch case
+WGRAD_CASES = [
+    (2, 16, 24, 14, 14, 1), (1, 32, 8, 11, 11, 0), (2, 8, 16, 9, 9, 2), (3, 40, 72, 13, 17, 1),
+    (1, 64, 64, 56, 56, 1), (1, 512, 512, 7, 7, 1), (32, 64, 64, 56, 56, 1),
+    (32, 256, 256, 14, 14, 1), (2, 3, 64, 224, 224, 1),
+]
+
+
+@pytest.mark.parametrize("B,C,K,H,W,pad", WGRAD_CASES)
+@pytest.mark.parametrize("gdt", ["f16", "f32"])
+def test_weight_grad_matches_fp64(oracle, B, C, K, H, W, pad, gdt):
+    """nova_weight_grad (fp32 Winograd-domain products reduced over the tiles)
+    against the fp64 direct gradient of the same fp16 input: rel-L2 <= 1e-4
+    and max-abs <= 1e-4 of the largest entry (the reference's bar for grad
+    weight is 0.15, tests/test_correctness.py:164). The output gradient comes
+    in fp16 or fp32; the result is deterministic."""
+    from nova_winograd.ops import check, get_lib
+
+    print(f"[wgrad] B={B} C={C} K={K} H={H} W={W} pad={pad} dy={gdt}", flush=True)
+    lib = get_lib()
+    g = torch.Generator().manual_seed(B + C + K + H)
+    x = torch.randn(B, C, H, W, generator=g).half()
+    Ho, Wo = H + 2 * pad - 2, W + 2 * pad - 2
+    dy = torch.randn(B, K, Ho, Wo, generator=g) * 1e-3
+    if gdt == "f16":
+        dy = dy.half()
+    xd, gd = x.to(DEV), dy.to(DEV)
+    outs = []
+    h = lib.nova_create()
+    try:
+        for _ in range(2):
+            gw = torch.full((K, C, 3, 3), float("nan"), device=DEV)
+            lib.nova_weight_grad(h, xd.data_ptr(), gd.data_ptr(), gw.data_ptr(), B, C, K, H, W,
+                                 pad, 1 if gdt == "f32" else 0)
+            check()
+            outs.append(gw)
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    assert torch.equal(outs[0], outs[1]), "not deterministic"
+    n = min(B, 4)  # the fp64 truth on the first images of a large batch ...
+    if n < B:  # ... against the GPU on those images alone
+        h = lib.nova_create()
+        try:
+            gw_n = torch.empty(K, C, 3, 3, device=DEV)
+            lib.nova_weight_grad(h, xd.data_ptr(), gd.data_ptr(), gw_n.data_ptr(), n, C, K, H, W,
+                                 pad, 1 if gdt == "f32" else 0)
+            check()
+            torch.cuda.synchronize()
+        finally:
+            lib.nova_destroy(h)
+    else:
+        gw_n = outs[0]
+    got = gw_n.cpu().numpy().astype(np.float64)
+    want = oracle.weight_grad(x[:n].numpy(), dy[:n].float().numpy(), pad)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    worst = np.abs(got - want).max() / np.abs(want).max()
+    print(f"[wgrad] rel-L2 {rel:.2e}, max-abs/max {worst:.2e}", flush=True)
+    assert np.isfinite(got).all()
+    assert rel <= 1e-4
+    assert worst <= 1e-4
+    if n < B:  # the whole batch: linear in the images, so it is the sum over sub-batches
+        rest = torch.empty(K, C, 3, 3, device=DEV)
+        h = lib.nova_create()
+        try:
+            lib.nova_weight_grad(h, xd[n:].contiguous().data_ptr(), gd[n:].contiguous().data_ptr(),
+                                 rest.data_ptr(), B - n, C, K, H, W, pad,
+                                 1 if gdt == "f32" else 0)
+            check()
+            torch.cuda.synchronize()
+        finally:
+            lib.nova_destroy(h)
+        # each side is within ~3e-5 of the exact gradient (fp32 sums over
+        # different partitions of the tiles)
+        total = (gw_n + rest).double()
+        full = outs[0].double()
+        assert ((full - total).norm() / full.norm()).item() <= 1e-4
+
+
+def test_weight_grad_empty_batch_is_zero():
+    from nova_winograd.ops import check, get_lib
+
+    lib = get_lib()
+    gw = torch.full((8, 4, 3, 3), 7.0, device=DEV)
+    h = lib.nova_create()
+    try:
+        lib.nova_weight_grad(h, None, None, gw.data_ptr(), 0, 4, 8, 9, 9, 1, 0)
+        check()
+        torch.cuda.synchronize()
+    finally:
+        lib.nova_destroy(h)
+    assert not gw.any()
+
+
+def test_trainable_weight_grad_on_hip_path(oracle):
+    """The module's backward takes grad weight from nova_weight_grad: it
+    matches the fp64 gradient of the fp16 input the forward convolved, with
+    an fp16 output gradient as autograd delivers it, and the bias gradient is
+    the channel sum."""
+    from nova_winograd import NovaWinogradConv2dTrainable
+
+    torch.manual_seed(14)
+    conv = NovaWinogradConv2dTrainable(24, 40, kernel_size=3, padding=1, bias=True).to(DEV)
+    x = torch.randn(3, 24, 20, 20, device=DEV)
+    y = conv(x)
+    go = (torch.randn_like(y.float()) * 0.01).half()
+    y.backward(go)
+    torch.cuda.synchronize()
+    want = oracle.weight_grad(x.half().cpu().numpy(), go.float().cpu().numpy(), 1)
+    got = conv.weight.grad.double().cpu().numpy()
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) <= 1e-4
+    gb = go.float().sum(dim=(0, 2, 3))
+    assert torch.allclose(conv.bias.grad, gb, rtol=1e-5, atol=1e-6)

@@ -43,7 +43,8 @@ def test_product_tables_equal_derivation():
     """The product library's compiled-in tables (a separate copy) match."""
     text = open(os.path.join(ROOT, "nova-wino-amd_amd", "csrc", "nova_tables.h")).read()
     A32, B32, G32, Ah, Bh = D.fp32_tables()
-    for name, want, shape in [("kG", G32, (8, 3)), ("kAh", Ah, (6, 8)), ("kBh", Bh, (8, 8))]:
+    for name, want, shape in [("kG", G32, (8, 3)), ("kAh", Ah, (6, 8)), ("kBh", Bh, (8, 8)),
+                              ("kA", A32, (6, 8)), ("kB", B32, (8, 8))]:
         got = _parse_c_table(text, name, *shape)
         assert np.array_equal(np.array(want, np.float32).view(np.uint32), got.view(np.uint32)), name
 
@@ -332,3 +333,22 @@ def test_direct_conv_matches_torch(oracle):
                                          torch.from_numpy(w.astype(np.float64)), padding=pad)
         got = oracle.direct_conv2d(x, w, pad)
         assert np.allclose(got, ref.numpy(), rtol=0, atol=1e-9)
+
+
+@pytest.mark.parametrize("B,C,K,H,W,pad", [(2, 3, 5, 9, 7, 1), (1, 4, 2, 6, 11, 0),
+                                           (3, 2, 3, 5, 5, 2)])
+def test_weight_grad_matches_torch_fp64(oracle, B, C, K, H, W, pad):
+    """The oracle's weight gradient (fp64 direct sum) equals PyTorch's
+    float64 conv2d_weight on the same fp16 input and fp32 output gradient,
+    and a planted shift of the filter index would not."""
+    import torch
+
+    g = torch.Generator().manual_seed(B * 100 + C)
+    x = torch.randn(B, C, H, W, generator=g).half()
+    Ho, Wo = H + 2 * pad - 2, W + 2 * pad - 2
+    dy = torch.randn(B, K, Ho, Wo, generator=g)
+    got = oracle.weight_grad(x.numpy(), dy.numpy(), pad)
+    want = torch.nn.grad.conv2d_weight(x.double(), (K, C, 3, 3), dy.double(),
+                                       padding=pad).numpy()
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    assert not np.allclose(np.roll(got, 1, axis=3), want, rtol=1e-6, atol=1e-6)
