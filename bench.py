@@ -51,6 +51,7 @@ BATCHES = [1, 32]
 PEAK_HBM_GBS = 8000.0
 PEAK_FP16_TFLOPS = 2500.0
 KIND_NAMES = ["input", "gemm", "output", "fused"]
+PATH_NAMES = {1: "3-pass", 2: "fused_rows", 3: "fused_block", 4: "windowed", 5: "fused_small"}
 
 
 def log(*a):
@@ -635,7 +636,7 @@ def extra_measurements(runs, lib, torch, nn, nw, reps):
     """Per-layer NOVA vs MIOpen on the other BASELINE configs and the full
     random-init ResNet-50 forward with and without surgery."""
     dev = torch.device("cuda:0")
-    path_names = {1: "3-pass", 2: "fused_rows", 3: "fused_block"}
+    path_names = PATH_NAMES
     out = {"layers": []}
     for name, B, C, K, H in EXTRA_LAYERS:
         torch.manual_seed(0)
@@ -891,7 +892,7 @@ def main():
         for r in runs:
             mod, mio, x = r["mod"], r["mio"], r["x"]
             r["nova_ms"] = time_region(lambda: mod(x), args.layer_reps, torch)
-            r["path"] = {1: "3-pass", 2: "fused_rows", 3: "fused_block"}.get(lib.nova_get_last_path(mod._handle.h), "?")
+            r["path"] = PATH_NAMES.get(lib.nova_get_last_path(mod._handle.h), "?")
             if not args.no_miopen:
                 r["miopen_ms"] = time_region(lambda: mio(x), args.layer_reps, torch)
             if not args.no_graph:

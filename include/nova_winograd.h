@@ -132,7 +132,10 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
 
 /* Path selection: 0 = automatic (default), 1 = force 3-pass, 2 = force the
  * fused kernel split by position row (small batches), 3 = force the fused
- * tile-block kernel (few channels, batch > 1), 4 = windowed 3-pass: the batch
+ * tile-block kernel (few channels, batch > 1), 5 = force the small-problem
+ * fused kernel (C, K <= 64: one launch of 2 tiles x 16 output channels per
+ * workgroup, chosen automatically while its grid is at most two workgroups
+ * per CU, e.g. batch 1), 4 = windowed 3-pass: the batch
  * runs in windows of whole images whose V + M fit the window budget
  * (nova_set_window_bytes), each window's three kernels back to back -- the
  * BP-windowed pipeline of /root/reference/tests/test_bp_tiled.hip:482-571,
@@ -140,8 +143,8 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
  * 3-pass and reports an error. The fused kernels read a second, fragment-
  * ordered copy of the transformed filter (device memory the size of U); a
  * handle builds it in nova_set_weights when a fused kernel can run (C, K <= 64
- * on the automatic path, or 2 / 3 already forced), here when 2 or 3 is forced
- * after the weights, and otherwise never. */
+ * on the automatic path, or 2 / 3 / 5 already forced), here when 2, 3 or 5 is
+ * forced after the weights, and otherwise never. */
 NOVA_API void nova_set_path(nova_handle_t h, int path);
 /* V + M bytes per window of path 4 (0 = default, 4 MiB, the reference's
  * budget; at least one image per window). No counterpart in the reference,
@@ -171,7 +174,8 @@ NOVA_API void nova_set_layout(nova_handle_t h, int nhwc);
  * reference (a residual there is a separate elementwise op). */
 NOVA_API void nova_set_residual(nova_handle_t h, const void* d_residual_f16);
 /* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused
- * (position rows), 3 = fused (tile blocks), 4 = windowed 3-pass. */
+ * (position rows), 3 = fused (tile blocks), 4 = windowed 3-pass, 5 = fused
+ * (small problems). */
 NOVA_API int nova_get_last_path(nova_handle_t h);
 
 /* No counterpart in the reference. nova_forward for callers that cannot

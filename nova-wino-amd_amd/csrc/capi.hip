@@ -298,9 +298,21 @@ int64_t window_images(const Handle* Hd, const Shape& s) {
     return std::max<int64_t>(1, Hd->window_bytes / per_img);
 }
 
+bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
+    const int64_t Bc = sub_batch(Hd, s);
+    if (!fused_fits(Bc * Hd->C * s.H * s.W, u_frag_elems(Hd->K, Hd->Cp),
+                    Bc * Hd->K * s.Ho * s.Wo))
+        return false;
+    return fused_small_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, p);
+}
+
 int choose_path(const Handle* Hd, const Shape& s) {
     if (Hd->path_pref == 1) return 1;
     if (Hd->path_pref == 4) return 4;
+    if (Hd->path_pref == 5) {
+        FusedSmallPlan p;
+        return fused_small_plan_for(Hd, s, &p) ? 5 : 1;
+    }
     if (Hd->path_pref == 2) {
         if (Hd->nhwc) return 1;  // the position-row kernel reads and writes NCHW only
         FusedPlan p;
@@ -325,6 +337,15 @@ int choose_path(const Handle* Hd, const Shape& s) {
     // vs 25.7, B=44 46.7 vs 50.5, B=56 55.0 vs 51.4, B=112 102.8 vs 91.4;
     // 64@28^2 B=64 29.1 vs 25.6; 32@56^2 B=8 19.7 vs 15.0; 48->40@13^2 B=128
     // 22.8 vs 24.2.
+    // Small problems (the small-problem kernel's grid at most two workgroups
+    // per CU): one launch of that kernel. Measured on MI355X, us, three-pass
+    // vs small kernel: conv2_x B=1 10.4 vs 7.8, B=2 12.4 vs 10.4 (B=4 17.0 vs
+    // 18.2: three-pass); 32@56^2 B=4 12.7 vs 9.7; 48->40@13^2 B=32 13.7 vs
+    // 10.2 (B=128 22.8 vs 30.9); 64@112^2 B=1 15.3 vs 16.0 (724 workgroups).
+    FusedSmallPlan sp;
+    if (Hd->C <= 64 && Hd->K <= 64 && fused_small_plan_for(Hd, s, &sp) &&
+        sp.grid <= 2 * (int64_t)Hd->cus)
+        return 5;
     FusedBlockPlan bp;
     if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
@@ -441,9 +462,9 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     if (no_alloc) {
         // the position-row kernel needs an allocated M buffer and counters,
         // and a fragment copy not yet built would be allocated here
-        if (path == 2 || (path == 3 && !Hd->uf_ready)) path = 1;
+        if (path == 2 || ((path == 3 || path == 5) && !Hd->uf_ready)) path = 1;
         const int64_t per_img = 2 * (int64_t)64 * (Hd->Cp + Hd->K) * s_all.nh * s_all.nw;
-        if (path != 3 && per_img > (int64_t)NOVA_NOALLOC_SCRATCH_BYTES - 256) {
+        if ((path == 1 || path == 4) && per_img > (int64_t)NOVA_NOALLOC_SCRATCH_BYTES - 256) {
             set_error(kErrWorkspace,
                       "%s: one image needs %lld bytes of workspace; the allocation-free "
                       "forward holds %lld",
@@ -451,12 +472,12 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             return;
         }
         // V, then M at the next 256-byte boundary
-        if (path != 3)
+        if (path == 1 || path == 4)
             chunk = std::min<int64_t>(chunk, (NOVA_NOALLOC_SCRATCH_BYTES - 256) / per_img);
     }
-    const bool fused = path == 2 || path == 3;
+    const bool fused = path == 2 || path == 3 || path == 5;
     if (fused && !ensure_uf(Hd)) return;
-    if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3)) {
+    if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3 || Hd->path_pref == 5)) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
     Hd->last_path = path;
@@ -499,7 +520,29 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         uint16_t* yy = static_cast<uint16_t*>(y) + b0 * y_img;
         Epilogue ep = Hd->ep;  // the residual follows the output's sub-batch
         if (ep.residual) ep.residual += b0 * y_img;
-        if (path == 3) {
+        if (path == 5) {
+            const hipStream_t st = Hd->stream;
+            const uint16_t* U = Hd->Uf;
+            const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+            const bool nhwc = Hd->nhwc != 0;
+            FusedSmallPlan sp;
+            if (!fused_small_plan((int)s.B, C, K, Cp, s.nh, s.nw, &sp)) {
+                set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
+                return;
+            }
+            auto fz = [=]() {
+                return launch_fused_small(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
+                                          s.Ho, s.Wo, sp, st, ep, nhwc);
+            };
+            if (b0 == 0 && !no_alloc) {
+                for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
+                pf.last[kKindFused] = fz;
+            }
+            const size_t e0 = no_alloc ? SIZE_MAX : pf.arm();
+            const bool ok = hip_ok(fz(), "fused small kernel");
+            pf.done(kKindFused, e0, "fused_small_kernel");
+            if (!ok) return;
+        } else if (path == 3) {
             const hipStream_t st = Hd->stream;
             const uint16_t* U = Hd->Uf;
             const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
@@ -632,7 +675,7 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
     H->ready = hip_ok(launch_filter_transform_gemm(d_weight, w_f16, H->U, K, C, Cp, H->stream),
                       "filter transform");
     const bool fused_possible = (C <= 64 && K <= 64 && H->path_pref == 0) ||
-                                H->path_pref == 2 || H->path_pref == 3;
+                                H->path_pref == 2 || H->path_pref == 3 || H->path_pref == 5;
     if (H->ready && fused_possible) H->ready = ensure_uf(H);
 }
 
@@ -841,12 +884,13 @@ void nova_set_stream(nova_handle_t h, void* stream) {
 void nova_set_path(nova_handle_t h, int path) {
     Handle* H = as_handle(h, "nova_set_path");
     if (!H) return;
-    if (path < 0 || path > 4) {
-        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2, 3 or 4");
+    if (path < 0 || path > 5) {
+        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2, 3, 4 or 5");
         return;
     }
     H->path_pref = path;
-    if ((path == 2 || path == 3) && H->ready) ensure_uf(H);  // fused forced after the weights
+    if ((path == 2 || path == 3 || path == 5) && H->ready)
+        ensure_uf(H);  // fused forced after the weights
 }
 
 void nova_set_window_bytes(nova_handle_t h, long long bytes) {
@@ -897,7 +941,7 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     Shape s;
     if (!make_shape(Hd, batch, H, W, pad, &s, "nova_workspace_bytes")) return -1;
     const int path = Hd->ready ? choose_path(Hd, s) : 1;
-    if (path == 2 || path == 3) return 0;
+    if (path == 2 || path == 3 || path == 5) return 0;
     int64_t chunk = std::max<int64_t>(1, batch_chunk(Hd, s));
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s));
     const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;

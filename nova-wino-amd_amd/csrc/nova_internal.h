@@ -149,6 +149,22 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
                               int Wo, const FusedBlockPlan& p, hipStream_t s,
                               Epilogue ep = Epilogue());
 
+// Small-problem variant (2 tiles x 16 output channels x all positions per
+// workgroup, every workgroup recomputing its tiles' input transform; no
+// scratch, no hand-off): C, K <= 64 when the other kernels' grids cannot
+// fill the chip (batch 1).
+struct FusedSmallPlan {
+    int tiles;  // tiles per workgroup
+    int ntg;    // tile groups per image
+    int nkb;    // 16-channel output blocks
+    int64_t grid;
+};
+bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, FusedSmallPlan* p);
+hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
+                              int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
+                              int Wo, const FusedSmallPlan& p, hipStream_t s,
+                              Epilogue ep = Epilogue(), bool nhwc = false);
+
 // ---- weight gradient (Winograd domain, fp32) --------------------------------
 // Plan of a weight-gradient computation: images per sub-batch (the fp32
 // transformed operands stay below 2^31 bytes each and 1 GiB together), the

@@ -55,20 +55,24 @@ def _forward(lib, path, x, w, pad):
     return y, took
 
 
-# (B, C, K, H, expected automatic path): the library's cost model, fused
-# ~(3 + 10 us per 32-channel chunk) per wave of workgroups against three-pass
-# ~10 us + its bytes at 5 TB/s
+# (B, C, K, H, expected automatic path): the small-problem kernel (5) while
+# its grid is at most two workgroups per CU, else the library's cost model,
+# fused ~(3 + 10 us per 32-channel chunk) per wave of workgroups against
+# three-pass ~10 us + its bytes at 5 TB/s
 AUTO_CASES = [
     (32, 64, 64, 56, 3),   # ResNet-50 conv2_x, B=32: one wave, fused 23 vs 36 us
     (48, 64, 64, 56, 3),   # two waves, 46 vs 49 us (measured 50.5 vs 49.1: a near miss)
     (64, 64, 64, 56, 3),   # two waves, 46 vs 62 us
     (128, 64, 64, 56, 3),  # four waves
     (16, 64, 64, 56, 3),   # 112 workgroups, one wave: 23 vs 23.1 us
-    (8, 64, 64, 56, 1),    # 56 workgroups: 23 vs 16.5 us
+    (8, 64, 64, 56, 1),    # 56 workgroups: 23 vs 16.5 us (small kernel: 1600 workgroups)
     (8, 32, 32, 56, 3),    # one 32-channel chunk: 13 vs 16 us
     (128, 48, 40, 13, 1),  # small images: 23 vs 16 us
     (32, 128, 128, 28, 1),  # conv3_x: more than 64 channels, three-pass
-    (1, 64, 64, 56, 1),    # B=1: three-pass
+    (1, 64, 64, 56, 5),    # B=1: the small-problem kernel (200 workgroups)
+    (2, 64, 64, 56, 5),    # 400 workgroups
+    (4, 64, 64, 56, 1),    # 800 workgroups: three-pass
+    (32, 48, 40, 13, 5),   # small images: 480 workgroups
 ]
 
 

@@ -61,16 +61,17 @@ def test_nhwc_equals_nchw(B, C, K, H, pad):
     torch.manual_seed(12)
     x = torch.randn(B, C, H, H, device=DEV).half()
     w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
-    y_ref, took_ref = _run(x, w, pad, False, path=1)
     y, took = _run(x.contiguous(memory_format=CL), w, pad, True)
-    assert took == 1
+    assert took in (1, 5)  # three-pass, or the small-problem kernel for small grids
+    y_ref, took_ref = _run(x, w, pad, False, path=took)  # the same path in NCHW
+    assert took_ref == took
     assert y.is_contiguous(memory_format=CL)
     assert torch.equal(y, y_ref)
     # epilogue in NHWC: bias, residual (channels-last), ReLU
     bias = (torch.randn(K, device=DEV) * 0.5).half()
     res = torch.randn_like(y_ref).contiguous(memory_format=CL)
     y_e, _ = _run(x.contiguous(memory_format=CL), w, pad, True, bias=bias, relu=1, res=res)
-    yb_ref, _ = _run(x, w, pad, False, bias=bias, path=1)
+    yb_ref, _ = _run(x, w, pad, False, bias=bias, path=took)
     assert torch.equal(y_e, torch.relu(yb_ref + res))
 
 
