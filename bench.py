@@ -184,7 +184,8 @@ KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_
 FAMILY_OF_KIND = {0: "input_transform_kernel", 1: "wgemm", 2: "output_transform_kernel"}
 
 NOVA_KERNELS = ["input_transform_kernel", "wgemm", "output_transform_kernel",
-                "fused_block_kernel", "fused_kernel<1>", "fused_kernel<2>", "fused_kernel<4>"]
+                "fused_block_kernel", "fused_small_kernel", "fused_kernel<1>", "fused_kernel<2>",
+                "fused_kernel<4>"]
 
 
 def _name_keys(name):
@@ -248,7 +249,8 @@ def mfma_from(pmc_dir, bench_json, out_path, cus=256):
                       "SQ_VALU_MFMA_BUSY_CYCLES / (bench avg_launch_us x "
                       f"{CLOCK_GHZ} GHz x {cus} CUs x 4 SIMDs)",
             "peak_tflops": PEAK_FP16_TFLOPS, "clock_ghz": CLOCK_GHZ, "kernels": []}
-    for name in ("wgemm", "fused_block_kernel", "fused_kernel<1>", "fused_kernel<2>",
+    for name in ("wgemm", "fused_block_kernel", "fused_small_kernel", "fused_kernel<1>",
+                 "fused_kernel<2>",
                  "fused_kernel<4>"):
         sel = {c: [r for r in per[c] if any(k in r[0] for k in _name_keys(name))]
                for c in MFMA_COUNTERS}
