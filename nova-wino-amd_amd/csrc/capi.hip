@@ -303,7 +303,7 @@ bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
     if (!fused_fits(Bc * Hd->C * s.H * s.W, u_frag_elems(Hd->K, Hd->Cp),
                     Bc * Hd->K * s.Ho * s.Wo))
         return false;
-    return fused_small_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, p);
+    return fused_small_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, p);
 }
 
 int choose_path(const Handle* Hd, const Shape& s) {
@@ -339,9 +339,9 @@ int choose_path(const Handle* Hd, const Shape& s) {
     // 22.8 vs 24.2.
     // Small problems (the small-problem kernel's grid at most two workgroups
     // per CU): one launch of that kernel. Measured on MI355X, us, three-pass
-    // vs small kernel: conv2_x B=1 10.4 vs 7.8, B=2 12.4 vs 10.4 (B=4 17.0 vs
-    // 18.2: three-pass); 32@56^2 B=4 12.7 vs 9.7; 48->40@13^2 B=32 13.7 vs
-    // 10.2 (B=128 22.8 vs 30.9); 64@112^2 B=1 15.3 vs 16.0 (724 workgroups).
+    // vs small kernel: conv2_x B=1 10.4 vs 7.5, B=2 12.0 vs 10.4 (B=4 16.9 vs
+    // 18.0: three-pass); 32@56^2 B=4 12.5 vs 9.7; 48->40@13^2 B=32 13.4 vs
+    // 10.2 (B=128 22.9 vs 31.0); 64@112^2 B=1 15.7 vs 16.1 (724 workgroups).
     FusedSmallPlan sp;
     if (Hd->C <= 64 && Hd->K <= 64 && fused_small_plan_for(Hd, s, &sp) &&
         sp.grid <= 2 * (int64_t)Hd->cus)
@@ -526,7 +526,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
             const bool nhwc = Hd->nhwc != 0;
             FusedSmallPlan sp;
-            if (!fused_small_plan((int)s.B, C, K, Cp, s.nh, s.nw, &sp)) {
+            if (!fused_small_plan((int)s.B, C, K, Cp, s.nh, s.nw, Hd->cus, &sp)) {
                 set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
                 return;
             }

@@ -11,15 +11,16 @@
 // group's input transform (cheap at C <= 64) instead of sharing it, so there
 // are B * ceil(P / T) * ceil(K / 16) independent workgroups (200 at conv2_x
 // batch 1), each on the latency chain of one kernel:
-//   * the wave's U fragments (fragment-ordered U, 16 output channels x 8
-//     positions x 2 channel chunks) are requested first and stay in flight
+//   * the wave's U fragments (fragment-ordered U, 16 output channels x the
+//     wave's positions x 2 channel chunks) are requested first and stay in flight
 //     during the transform;
 //   * input transform, lane-parallel (8 lanes per patch, row pass, LDS
 //     transpose, column pass: the chains of input_lp_kernel, so V is
-//     bit-identical), T rounds of 64 channels; V goes to LDS as
+//     bit-identical), 64 channels x NTH / 512 tiles per round; V goes to LDS as
 //     v_mfma_f32_16x16x32_f16 B operands with T tile slots (lanes of the
 //     empty slots read a zero block);
-//   * products: wave w multiplies positions 8w .. 8w+7, one MFMA per position
+//   * products: each of the NTH / 64 waves multiplies 64 / (NTH / 64)
+//     consecutive positions, one MFMA per position
 //     and 32-channel chunk, in the operand order of the fused tile-block
 //     kernel (so M is bit-identical to that kernel's);
 //   * M rounded to fp16 (the reference's rounding point,
@@ -38,7 +39,6 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kSmThreads = 512;          // 8 waves: one per position row
 constexpr int kSmK = 16;                 // output channels per workgroup
 constexpr int kSmPitch = 72;             // floats per row of the transpose buffers
 constexpr int kSmOob = (int)0x80000000;  // out-of-range byte offset: loads 0, stores dropped
@@ -81,10 +81,16 @@ __device__ __forceinline__ int sm_v_index(int pos, int c, int t) {
     return sm_v_base<T>(pos, chunk, (cc >> 2) & 3, t) + ((cc >> 4) & 1) * 4 + (cc & 3);
 }
 
-template <int T, bool kNhwc>
-__global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a) {
+// NTH threads (512 or 1024): NTH / 512 tiles are transformed per round, each
+// wave multiplies 64 / (NTH / 64) positions.
+template <int T, int NTH, bool kNhwc>
+__global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
+    constexpr int kWaves = NTH / 64;
+    constexpr int kPpw = 64 / kWaves;                          // positions per wave
+    constexpr int kTpr = NTH / 512;                            // tiles per transform round
+    static_assert(T % kTpr == 0, "whole rounds");
     constexpr int kVHalves = 64 * sm_pos_halves<T>();          // V of the group's tiles
-    constexpr int kTpFloats = 64 * kSmPitch;                   // one transpose buffer
+    constexpr int kTpFloats = 64 * kSmPitch * kTpr;            // one transpose buffer
     __shared__ __align__(16) _Float16 vs[kVHalves + 8];        // + one zero block
     __shared__ __align__(16) float tps[2][kTpFloats];          // double-buffered transposes
     const int tid = threadIdx.x;
@@ -104,23 +110,26 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
     const __amdgpu_buffer_rsrc_t urs = sm_rsrc(a.U, a.u_bytes);
     const __amdgpu_buffer_rsrc_t yrs = sm_rsrc(a.y, a.y_bytes);
 
-    // ---- 0. this wave's U operands: positions 8w .. 8w+7, both chunks ----
-    h8 ua[8][2];
+    // ---- 0. this wave's U operands: positions kPpw*w .. +kPpw-1, both chunks ----
+    h8 ua[kPpw][2];
 #pragma unroll
-    for (int s = 0; s < 8; s++)
+    for (int s = 0; s < kPpw; s++)
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int pos = 8 * wave + s;
+            const int pos = kPpw * wave + s;
             const int off = j < a.nkp ? ((pos * a.nkt + kb) * a.nkp + j) * 1024 : kSmOob;
             ua[s][j] = __builtin_bit_cast(
                 h8, __builtin_amdgcn_raw_buffer_load_b128(urs, lane * 16, off, 0));
         }
 
-    // ---- 1. input columns: lane (channel c = tid / 8, column j), T tiles ----
-    const int c = tid >> 3, j = tid & 7;
-    float d[T][8];
+    // ---- 1. input columns: lane (channel c, column j) of tile slot
+    // ts = tid / 512 in each round (kTpr slots per round), T / kTpr rounds ----
+    const int c = (tid >> 3) & 63, j = tid & 7, ts = tid >> 9;
+    constexpr int kRounds = T / kTpr;
+    float d[kRounds][8];
 #pragma unroll
-    for (int t = 0; t < T; t++) {
+    for (int rd = 0; rd < kRounds; rd++) {
+        const int t = rd * kTpr + ts;
         const int tl = t0 + min(t, ntiles - 1);
         const int th = tl / a.nw, tw = tl - (tl / a.nw) * a.nw;
         const int w = 6 * tw - a.pad + j;
@@ -133,22 +142,23 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
         for (int i = 0; i < 8; i++) {
             const int h = 6 * th - a.pad + i;
             const int off = (ok && h >= 0 && h < a.H) ? base + h * rstep : kSmOob;
-            d[t][i] = (float)__builtin_bit_cast(
+            d[rd][i] = (float)__builtin_bit_cast(
                 _Float16, __builtin_amdgcn_raw_buffer_load_b16(xrs, off, 0, 0));
         }
     }
     if (tid < 2) *reinterpret_cast<unsigned long long*>(vs + kVHalves + 4 * tid) = 0ull;
 
-    // ---- 2. input transform, one tile per round (chains of input_lp_kernel) ----
+    // ---- 2. input transform, kTpr tiles per round (chains of input_lp_kernel) ----
 #pragma unroll
-    for (int t = 0; t < T; t++) {
-        float* tp = tps[t & 1] + c * kSmPitch;
+    for (int rd = 0; rd < kRounds; rd++) {
+        const int t = rd * kTpr + ts;
+        float* tp = tps[rd & 1] + (tid >> 3) * kSmPitch;
 #pragma unroll
         for (int r = 0; r < 8; r++) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], d[t][i], acc);
+                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], d[rd][i], acc);
             tp[r * 8 + j] = acc;
         }
         __syncthreads();
@@ -168,16 +178,16 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
     }
     __syncthreads();
 
-    // ---- 3. products: positions 8w .. 8w+7 ----
+    // ---- 3. products: positions kPpw*w .. +kPpw-1 ----
     const int tl = lane & 15, cg = lane >> 4;
-    f4 acc[8];
+    f4 acc[kPpw];
 #pragma unroll
-    for (int s = 0; s < 8; s++) acc[s] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < kPpw; s++) acc[s] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int jc = 0; jc < 2; jc++)
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const int pos = 8 * wave + s;
+        for (int s = 0; s < kPpw; s++) {
+            const int pos = kPpw * wave + s;
             const int vo = tl < T ? sm_v_base<T>(pos, jc, cg, tl) : kVHalves;
             const h8 vb = *reinterpret_cast<const h8*>(vs + vo);
             acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[s][jc], vb, acc[s], 0, 0, 0);
@@ -185,6 +195,7 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
 
     // ---- 4. M (fp16) to LDS as [kk][tile][position] (transpose buffer 0) ----
     static_assert(kSmK * T * 72 <= 2 * kTpFloats, "M fits in a transpose buffer");
+    static_assert(kSmK * T * kSmPitch <= kTpFloats, "output transposes fit in buffer 1");
     _Float16* ms = reinterpret_cast<_Float16*>(tps[0]);  // 16 x T x 72 halves
     __syncthreads();  // every wave is done with the transpose buffers' last round
     if (tl < T) {
@@ -192,8 +203,8 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
         for (int i = 0; i < 4; i++) {
             const int kk = 4 * cg + i;
 #pragma unroll
-            for (int s = 0; s < 8; s++)
-                ms[(kk * T + tl) * 72 + 8 * wave + s] = to_f16(acc[s][i]);
+            for (int s = 0; s < kPpw; s++)
+                ms[(kk * T + tl) * 72 + kPpw * wave + s] = to_f16(acc[s][i]);
         }
     }
     __syncthreads();
@@ -203,7 +214,7 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
     float* tq = tps[1];  // free since the transform (M is in tps[0]); 64 x kSmPitch floats
     const _Float16* res = a.residual;
     const __amdgpu_buffer_rsrc_t rrs = sm_rsrc(res, res ? a.y_bytes : 0);
-    for (int pr0 = 0; pr0 < kSmK * T; pr0 += 64) {
+    for (int pr0 = 0; pr0 < kSmK * T; pr0 += NTH / 8) {
         const int pr = pr0 + (tid >> 3);
         const int kk = pr / T, t = pr - (pr / T) * T;
         const bool live = pr < kSmK * T;
@@ -291,7 +302,7 @@ __global__ __launch_bounds__(kSmThreads, 1) void fused_small_kernel(SmallArgs a)
 
 }  // namespace
 
-bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, FusedSmallPlan* p) {
+bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus, FusedSmallPlan* p) {
     if (B < 1 || C < 1 || K < 1 || C > 64 || K > 64 || Cp > 64) return false;
     const int P = nh * nw;
     // 2 tiles per workgroup: measured at conv2_x batch 1 (100 tiles), one
@@ -301,6 +312,12 @@ bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, FusedSmallPla
     p->ntg = (P + p->tiles - 1) / p->tiles;
     p->nkb = (K + kSmK - 1) / kSmK;
     p->grid = (int64_t)B * p->ntg * p->nkb;
+    // 1024 threads (one transform round, 4 positions per wave) while every
+    // workgroup has a CU of its own (91 KB of LDS: one per CU); 512 threads
+    // (54 KB, two per CU) beyond. Measured, us, 1024 vs 512 threads:
+    // conv2_x B=1 (200 workgroups) 7.5 vs 7.8, 32@56^2 B=2 (200) 6.9 vs 7.3,
+    // 64@28^2 B=4 (208) 7.3 vs 7.8; conv2_x B=2 (400) 13.4 vs 10.4.
+    p->threads = p->grid <= (int64_t)cus ? 1024 : 512;
     return p->grid < ((int64_t)1 << 31);
 }
 
@@ -337,12 +354,20 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.bias = reinterpret_cast<const _Float16*>(ep.bias);
     a.relu = ep.relu;
     a.residual = reinterpret_cast<const _Float16*>(ep.residual);
-    const dim3 grid((unsigned)p.grid), block(kSmThreads);
-    if (p.tiles != 2) return hipErrorInvalidConfiguration;
-    if (nhwc)
-        launch(fused_small_kernel<2, true>, grid, block, s, a);
-    else
-        launch(fused_small_kernel<2, false>, grid, block, s, a);
+    const dim3 grid((unsigned)p.grid), block((unsigned)p.threads);
+    if (p.tiles != 2 || (p.threads != 512 && p.threads != 1024))
+        return hipErrorInvalidConfiguration;
+    if (p.threads == 1024) {
+        if (nhwc)
+            launch(fused_small_kernel<2, 1024, true>, grid, block, s, a);
+        else
+            launch(fused_small_kernel<2, 1024, false>, grid, block, s, a);
+    } else {
+        if (nhwc)
+            launch(fused_small_kernel<2, 512, true>, grid, block, s, a);
+        else
+            launch(fused_small_kernel<2, 512, false>, grid, block, s, a);
+    }
     return hipGetLastError();
 }
 

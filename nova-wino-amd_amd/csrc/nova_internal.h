@@ -157,9 +157,11 @@ struct FusedSmallPlan {
     int tiles;  // tiles per workgroup
     int ntg;    // tile groups per image
     int nkb;    // 16-channel output blocks
+    int threads;  // workgroup size: 512 or 1024
     int64_t grid;
 };
-bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, FusedSmallPlan* p);
+bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus,
+                      FusedSmallPlan* p);
 hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
                               int Wo, const FusedSmallPlan& p, hipStream_t s,

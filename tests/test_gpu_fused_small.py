@@ -7,7 +7,10 @@ tile-block kernel's operand order, so wherever the tile-block kernel runs the
 result must equal it bit for bit; everywhere it must match the oracle within
 the forward parity bar. Covered: batch 1 and small batches, C and K off the
 16/32 blocks (C = 3, 20, K = 8, 48), odd and non-square images, pads 0-2,
-channels-last, and the bias/residual/ReLU epilogue.
+channels-last, and the bias/residual/ReLU epilogue. A grid of at most one
+workgroup per CU runs 1024-thread workgroups, a larger one 512-thread
+workgroups; the cases with more than 256 workgroups (conv2_x at batch 2, the
+batch-9 case) take the second.
 """
 
 import numpy as np
@@ -53,6 +56,7 @@ CASES = [  # (B, C, K, H, W, pad)
     (1, 64, 8, 9, 9, 2),      # K = 8, pad 2
     (4, 40, 24, 28, 28, 1),
     (1, 64, 64, 7, 7, 1),     # fewer tiles than a group (P = 4)
+    (9, 24, 40, 30, 26, 0),   # 270 workgroups: the 512-thread variant, ragged K
 ]
 
 
@@ -78,7 +82,8 @@ def test_fused_small_matches_oracle_and_tile_block(oracle, B, C, K, H, W, pad):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("B,C,K,H,pad", [(1, 64, 64, 56, 1), (2, 32, 48, 20, 1), (1, 16, 64, 13, 0)])
+@pytest.mark.parametrize("B,C,K,H,pad", [(1, 64, 64, 56, 1), (2, 32, 48, 20, 1), (1, 16, 64, 13, 0),
+                                         (7, 32, 48, 28, 1)])
 def test_fused_small_channels_last_and_epilogue(B, C, K, H, pad):
     """NHWC in and out equals the NCHW result in the other memory format, bit
     for bit; bias/residual/ReLU equal the separate fp16 ops."""
