@@ -27,6 +27,7 @@
 // The transforms are the shared tile arithmetic (bit-identical to the
 // standalone kernels); products accumulate over 32-channel chunks in order.
 #include <algorithm>
+#include <type_traits>
 
 #include "nova_internal.h"
 #include "nova_tables.h"
@@ -103,7 +104,7 @@ constexpr int kNhwcPix = 36;  // 72 bytes: tiles 6 pixels apart fall in distinct
 constexpr int kNhwcTileP = 64 * 72 + 8;
 static_assert(16 * kNhwcTileP * 2 <= 160 * 1024, "NHWC M fits in LDS");
 
-template <int NJ, bool kNhwc>
+template <int NJ, bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     __shared__ __align__(16) unsigned char lds[kBLdsBytes];
     unsigned char* xs = lds;
@@ -360,6 +361,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
             output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
             const int tlo = t0 + to;
             const int oh = (tlo / a.nw) * 6, ow = (tlo - (tlo / a.nw) * a.nw) * 6;
+            const ChannelEpilogue<kEpi> epi(a.bias, k, relu0);
 #pragma unroll
             for (int r = 0; r < 6; r++) {
                 if (oh + r >= a.Ho) break;
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
                 for (int s = 0; s < 6; s++)
                     if (ow + s < a.Wo) {
                         const int off = 2 * (((b * a.Ho + oh + r) * a.Wo + ow + s) * a.K + k);
-                        _Float16 v = epilogue(out[r][s], a.bias, k, relu0);
+                        _Float16 v = epi(out[r][s]);
                         if (res)
                             v = add_residual(
                                 v,
@@ -393,6 +395,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
         output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
         const int oh = th * 6, ow = tw * 6;
         const int ybase = 2 * ((b * a.K + k) * a.Ho * a.Wo + ow);
+        const ChannelEpilogue<kEpi> epi(a.bias, k, relu0);
 #pragma unroll
         for (int r = 0; r < 6; r++) {
             const int row = ybase + 2 * (oh + r) * a.Wo;
@@ -401,10 +404,8 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 #pragma unroll
                 for (int s = 0; s < 6; s += 2) {
                     if (ow + s < a.Wo) {
-                        const unsigned lo =
-                            __builtin_bit_cast(uint16_t, epilogue(out[r][s], a.bias, k, relu0));
-                        const unsigned hi = __builtin_bit_cast(
-                            uint16_t, epilogue(out[r][s + 1], a.bias, k, relu0));
+                        const unsigned lo = __builtin_bit_cast(uint16_t, epi(out[r][s]));
+                        const unsigned hi = __builtin_bit_cast(uint16_t, epi(out[r][s + 1]));
                         unsigned v = lo | (hi << 16);
                         if (res)
                             v = add_residual2(
@@ -417,7 +418,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 #pragma unroll
                 for (int s = 0; s < 6; s++)
                     if (ow + s < a.Wo) {
-                        _Float16 v = epilogue(out[r][s], a.bias, k, relu0);
+                        _Float16 v = epi(out[r][s]);
                         if (res)
                             v = add_residual(
                                 v,
@@ -513,21 +514,27 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
                     : 0;
     a.cols = p.cols;
     const dim3 grid((unsigned)p.grid), block(kBT);
+    const bool epi = epilogue_needed(ep.bias, ep.relu, ep.residual);
+    auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
     if (p.nhwc) {
         if (a.xd != 0) return hipErrorInvalidValue;  // 16-byte loads need an aligned x
-        launch(fused_block_kernel<0, true>, grid, block, s, a);
+        epi ? go(fused_block_kernel<0, true, true>) : go(fused_block_kernel<0, true, false>);
         return hipGetLastError();
     }
+    auto go_nj = [&](auto nj) {
+        constexpr int NJ = decltype(nj)::value;
+        epi ? go(fused_block_kernel<NJ, false, true>) : go(fused_block_kernel<NJ, false, false>);
+    };
     switch (p.nj) {
-        case 2: launch(fused_block_kernel<2, false>, grid, block, s, a); break;
-        case 3: launch(fused_block_kernel<3, false>, grid, block, s, a); break;
-        case 4: launch(fused_block_kernel<4, false>, grid, block, s, a); break;
-        case 5: launch(fused_block_kernel<5, false>, grid, block, s, a); break;
-        case 6: launch(fused_block_kernel<6, false>, grid, block, s, a); break;
-        case 7: launch(fused_block_kernel<7, false>, grid, block, s, a); break;
-        case 8: launch(fused_block_kernel<8, false>, grid, block, s, a); break;
-        case 9: launch(fused_block_kernel<9, false>, grid, block, s, a); break;
-        case 10: launch(fused_block_kernel<10, false>, grid, block, s, a); break;
+        case 2: go_nj(std::integral_constant<int, 2>()); break;
+        case 3: go_nj(std::integral_constant<int, 3>()); break;
+        case 4: go_nj(std::integral_constant<int, 4>()); break;
+        case 5: go_nj(std::integral_constant<int, 5>()); break;
+        case 6: go_nj(std::integral_constant<int, 6>()); break;
+        case 7: go_nj(std::integral_constant<int, 7>()); break;
+        case 8: go_nj(std::integral_constant<int, 8>()); break;
+        case 9: go_nj(std::integral_constant<int, 9>()); break;
+        case 10: go_nj(std::integral_constant<int, 10>()); break;
         default: return hipErrorInvalidConfiguration;
     }
     return hipGetLastError();

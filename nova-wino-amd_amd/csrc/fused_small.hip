@@ -27,6 +27,7 @@
 //     nova_winograd_fused.hip:405) to LDS, then the output transform,
 //     lane-parallel (the chains of output_lp_kernel) with the epilogue.
 #include <algorithm>
+#include <type_traits>
 
 #include "nova_internal.h"
 #include "nova_tables.h"
@@ -83,7 +84,7 @@ __device__ __forceinline__ int sm_v_index(int pos, int c, int t) {
 
 // NTH threads (512 or 1024): NTH / 512 tiles are transformed per round, each
 // wave multiplies 64 / (NTH / 64) positions.
-template <int T, int NTH, bool kNhwc>
+template <int T, int NTH, bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     constexpr int kWaves = NTH / 64;
     constexpr int kPpw = 64 / kWaves;                          // positions per wave
@@ -241,13 +242,14 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
 #pragma unroll
             for (int q = 0; q < 8; q++) t8[q] = tp[r * 8 + q];
             _Float16 out[6];
+            const ChannelEpilogue<kEpi> epi(a.bias, k, res ? 0 : a.relu);
 #pragma unroll
             for (int s2 = 0; s2 < 6; s2++) {
                 float s0 = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 8; q++)
                     if (kAh[s2][q] != 0.0f) s0 = __builtin_fmaf(t8[q], kAh[s2][q], s0);
-                out[s2] = epilogue(s0, a.bias, k, res ? 0 : a.relu);
+                out[s2] = epi(s0);
             }
             if constexpr (kNhwc) {
                 const int pix = 2 * (((b * a.Ho + oh) * a.Wo + ow) * a.K + k);
@@ -357,17 +359,20 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
     const dim3 grid((unsigned)p.grid), block((unsigned)p.threads);
     if (p.tiles != 2 || (p.threads != 512 && p.threads != 1024))
         return hipErrorInvalidConfiguration;
-    if (p.threads == 1024) {
-        if (nhwc)
-            launch(fused_small_kernel<2, 1024, true>, grid, block, s, a);
+    auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
+    auto go_th = [&](auto nth) {
+        constexpr int N = decltype(nth)::value;
+        if (epilogue_needed(ep.bias, ep.relu, ep.residual))
+            nhwc ? go(fused_small_kernel<2, N, true, true>)
+                 : go(fused_small_kernel<2, N, false, true>);
         else
-            launch(fused_small_kernel<2, 1024, false>, grid, block, s, a);
-    } else {
-        if (nhwc)
-            launch(fused_small_kernel<2, 512, true>, grid, block, s, a);
-        else
-            launch(fused_small_kernel<2, 512, false>, grid, block, s, a);
-    }
+            nhwc ? go(fused_small_kernel<2, N, true, false>)
+                 : go(fused_small_kernel<2, N, false, false>);
+    };
+    if (p.threads == 1024)
+        go_th(std::integral_constant<int, 1024>());
+    else
+        go_th(std::integral_constant<int, 512>());
     return hipGetLastError();
 }
 

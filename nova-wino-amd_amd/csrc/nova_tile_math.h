@@ -37,6 +37,38 @@ __device__ __forceinline__ _Float16 epilogue(float v, const _Float16* bias, int 
     return h;
 }
 
+// epilogue() for one output channel, with the channel's bias read once. With
+// kEpi false the kernel was launched without bias and without a ReLU at this
+// stage (none, or one that follows a residual add), and the value is only
+// rounded to fp16: no per-value bias or ReLU code at all.
+template <bool kEpi>
+struct ChannelEpilogue {
+    bool hb = false;
+    float bk = 0.0f;
+    int relu = 0;
+    __device__ ChannelEpilogue(const _Float16* bias, int k, int relu_) {
+        if constexpr (kEpi) {
+            hb = bias != nullptr;
+            bk = hb ? (float)bias[k] : 0.0f;
+            relu = relu_;
+        }
+    }
+    __device__ _Float16 operator()(float v) const {
+        _Float16 h = to_f16(v);
+        if constexpr (kEpi) {
+            if (hb) h = to_f16((float)h + bk);
+            if (relu && (float)h < 0.0f) h = (_Float16)0.0f;
+        }
+        return h;
+    }
+};
+
+// Whether a launch needs ChannelEpilogue<true>: a bias, or a ReLU that is not
+// deferred to a residual add.
+inline bool epilogue_needed(const void* bias, int relu, const void* residual) {
+    return bias != nullptr || (relu != 0 && residual == nullptr);
+}
+
 // Residual stage of the epilogue, after the bias: h plus the residual value
 // r (fp16 + fp16 summed in fp32, rounded once -- a separate `y + residual` on
 // fp16 tensors), then the optional ReLU. With a residual the ReLU is applied

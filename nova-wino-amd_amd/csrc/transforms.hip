@@ -557,7 +557,7 @@ struct OutGeom {
                                                   // at most 2-way write conflicts
 };
 
-template <int TW, int kVW>
+template <int TW, int kVW, bool kEpi>
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
@@ -589,12 +589,11 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
         output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
                     out);
         _Float16* sp = sy + kk * G::kPlane + t * 6;
-        const int kb = k < K ? k : 0;
+        const ChannelEpilogue<kEpi> epi(bias, k < K ? k : 0, res ? 0 : relu);
 #pragma unroll
         for (int r = 0; r < 6; r++)
 #pragma unroll
-            for (int s = 0; s < 6; s++)
-                sp[r * G::kCols + s] = epilogue(out[r][s], bias, kb, res ? 0 : relu);
+            for (int s = 0; s < 6; s++) sp[r * G::kCols + s] = epi(out[r][s]);
     }
     __syncthreads();
 
@@ -678,7 +677,7 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
 // instruction writes 128 contiguous bytes and no LDS transpose is needed.
 // The epilogue (bias, residual in y's layout, ReLU) is applied per value.
 // ---------------------------------------------------------------------------
-template <int TW>
+template <int TW, bool kEpi>
 __global__ __launch_bounds__(256) void output_nhwc_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
@@ -709,6 +708,7 @@ __global__ __launch_bounds__(256) void output_nhwc_kernel(
     output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
                 out);
     const int oh = 6 * th, ow = 6 * tw;
+    const ChannelEpilogue<kEpi> epi(bias, k, res ? 0 : relu);
 #pragma unroll
     for (int r = 0; r < 6; r++) {
         if (oh + r >= Ho) break;
@@ -716,7 +716,7 @@ __global__ __launch_bounds__(256) void output_nhwc_kernel(
         for (int s2 = 0; s2 < 6; s2++) {
             if (ow + s2 >= Wo) break;
             const int off = 2 * (((b * Ho + oh + r) * Wo + ow + s2) * K + k);
-            _Float16 v = epilogue(out[r][s2], bias, k, res ? 0 : relu);
+            _Float16 v = epi(out[r][s2]);
             if (res)
                 v = add_residual(
                     v,
@@ -728,20 +728,30 @@ __global__ __launch_bounds__(256) void output_nhwc_kernel(
 }
 
 template <int TW>
-static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, _Float16* yh,
-                          int K, int Ho, int Wo, int nh, int nw, int ldm, int64_t pstride,
-                          int kblocks, int64_t m_bytes, int64_t y_bytes, const _Float16* bias,
-                          int relu, const _Float16* res) {
+static void launch_out_tw(int vw, bool epi, dim3 grid, hipStream_t s, const _Float16* Mh,
+                          _Float16* yh, int K, int Ho, int Wo, int nh, int nw, int ldm,
+                          int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
+                          const _Float16* bias, int relu, const _Float16* res) {
     const dim3 block(256);
-    if (vw == 4)
-        launch(output_transform_kernel<TW, 4>, grid, block, s,
-            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
-    else if (vw == 2)
-        launch(output_transform_kernel<TW, 2>, grid, block, s,
-            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
-    else
-        launch(output_transform_kernel<TW, 1>, grid, block, s,
-            Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes, y_bytes, bias, relu, res);
+    auto go = [&](auto kernel) {
+        launch(kernel, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes,
+               y_bytes, bias, relu, res);
+    };
+    if (epi) {
+        if (vw == 4)
+            go(output_transform_kernel<TW, 4, true>);
+        else if (vw == 2)
+            go(output_transform_kernel<TW, 2, true>);
+        else
+            go(output_transform_kernel<TW, 1, true>);
+    } else {
+        if (vw == 4)
+            go(output_transform_kernel<TW, 4, false>);
+        else if (vw == 2)
+            go(output_transform_kernel<TW, 2, false>);
+        else
+            go(output_transform_kernel<TW, 1, false>);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -755,7 +765,7 @@ static void launch_out_tw(int vw, dim3 grid, hipStream_t s, const _Float16* Mh, 
 // else six halves; rows past Ho and columns past Wo are skipped).
 // Workgroup = 4 waves = 32 output channels of one tile.
 // ---------------------------------------------------------------------------
-template <bool kNhwc>
+template <bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(256) void output_lp_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int nkg, int64_t m_bytes, int64_t y_bytes, int pairs,
@@ -796,13 +806,14 @@ __global__ __launch_bounds__(256) void output_lp_kernel(
 #pragma unroll
         for (int q = 0; q < 8; q++) t[q] = tp[r * 8 + q];
         _Float16 out[6];
+        const ChannelEpilogue<kEpi> epi(bias, k, res ? 0 : relu);
 #pragma unroll
         for (int s2 = 0; s2 < 6; s2++) {
             float acc = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; q++)
                 if (kAh[s2][q] != 0.0f) acc = __builtin_fmaf(t[q], kAh[s2][q], acc);
-            out[s2] = epilogue(acc, bias, k, res ? 0 : relu);
+            out[s2] = epi(acc);
         }
         const int ow = 6 * tw;
         const __amdgpu_buffer_rsrc_t rrs = make_rsrc(res, res ? y_bytes : 0);
@@ -871,18 +882,17 @@ static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K,
                         3) == 0)
                           ? 1
                           : 0;
+    auto go = [&](auto kernel) {
+        launch(kernel, dim3((unsigned)items), dim3(256), s, reinterpret_cast<const _Float16*>(M),
+               reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw, ldm, pstride, nkg,
+               2 * 64 * pstride, y_bytes, pairs, reinterpret_cast<const _Float16*>(ep.bias),
+               ep.relu, reinterpret_cast<const _Float16*>(ep.residual));
+    };
+    const bool epi = epilogue_needed(ep.bias, ep.relu, ep.residual);
     if (nhwc)
-        launch(output_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
-            reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
-            ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
-            reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
-            reinterpret_cast<const _Float16*>(ep.residual));
+        epi ? go(output_lp_kernel<true, true>) : go(output_lp_kernel<true, false>);
     else
-        launch(output_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
-            reinterpret_cast<const _Float16*>(M), reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw,
-            ldm, pstride, nkg, 2 * 64 * pstride, y_bytes, pairs,
-            reinterpret_cast<const _Float16*>(ep.bias), ep.relu,
-            reinterpret_cast<const _Float16*>(ep.residual));
+        epi ? go(output_lp_kernel<false, true>) : go(output_lp_kernel<false, false>);
     return hipGetLastError();
 }
 
@@ -904,15 +914,17 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
         const _Float16* bias = reinterpret_cast<const _Float16*>(ep.bias);
         const _Float16* res = reinterpret_cast<const _Float16*>(ep.residual);
         const dim3 grid((unsigned)nblocks), block(256);
+        auto go = [&](auto kernel) {
+            launch(kernel, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+                   2 * 64 * pstride, y_bytes, bias, ep.relu, res);
+        };
+        const bool epi = epilogue_needed(bias, ep.relu, res);
         if (tw == 2)
-            launch(output_nhwc_kernel<2>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                   kblocks, 2 * 64 * pstride, y_bytes, bias, ep.relu, res);
+            epi ? go(output_nhwc_kernel<2, true>) : go(output_nhwc_kernel<2, false>);
         else if (tw == 4)
-            launch(output_nhwc_kernel<4>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                   kblocks, 2 * 64 * pstride, y_bytes, bias, ep.relu, res);
+            epi ? go(output_nhwc_kernel<4, true>) : go(output_nhwc_kernel<4, false>);
         else
-            launch(output_nhwc_kernel<8>, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride,
-                   kblocks, 2 * 64 * pstride, y_bytes, bias, ep.relu, res);
+            epi ? go(output_nhwc_kernel<8, true>) : go(output_nhwc_kernel<8, false>);
         return hipGetLastError();
     }
     const _Float16* bias = reinterpret_cast<const _Float16*>(ep.bias);
@@ -933,17 +945,18 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
     const _Float16* Mh = reinterpret_cast<const _Float16*>(M);
     _Float16* yh = reinterpret_cast<_Float16*>(y);
     const int64_t m_bytes = 2 * 64 * pstride;
+    const bool epi = epilogue_needed(bias, ep.relu, res);
     switch (tw) {
         case 2:
-            launch_out_tw<2>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+            launch_out_tw<2>(vw, epi, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
                              m_bytes, y_bytes, bias, ep.relu, res);
             break;
         case 4:
-            launch_out_tw<4>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+            launch_out_tw<4>(vw, epi, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
                              m_bytes, y_bytes, bias, ep.relu, res);
             break;
         default:
-            launch_out_tw<8>(vw, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+            launch_out_tw<8>(vw, epi, grid, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
                              m_bytes, y_bytes, bias, ep.relu, res);
             break;
     }
