@@ -133,9 +133,9 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
 /* Path selection: 0 = automatic (default), 1 = force 3-pass, 2 = force the
  * fused kernel split by position row (small batches), 3 = force the fused
  * tile-block kernel (few channels, batch > 1), 5 = force the small-problem
- * fused kernel (C, K <= 64: one launch of 2 tiles x 16 output channels per
- * workgroup, chosen automatically while its grid is at most two workgroups
- * per CU, e.g. batch 1), 4 = windowed 3-pass: the batch
+ * fused kernel (C, K <= 128: one launch of 2 tiles x 16 output channels per
+ * workgroup; chosen automatically for C, K <= 64 while its grid is at most
+ * two workgroups per CU, e.g. batch 1), 4 = windowed 3-pass: the batch
  * runs in windows of whole images whose V + M fit the window budget
  * (nova_set_window_bytes), each window's three kernels back to back -- the
  * BP-windowed pipeline of /root/reference/tests/test_bp_tiled.hip:482-571,

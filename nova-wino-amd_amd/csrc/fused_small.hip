@@ -1,7 +1,7 @@
-// Fused NOVA F(6,3) forward for small problems with few channels (C, K <= 64
-// at batch 1 and other grids too small to fill the chip): input transform,
-// the 64 Winograd-domain products and the output transform in ONE launch,
-// spread over many workgroups without any hand-off between them.
+// Fused NOVA F(6,3) forward for small problems (C, K <= 64 at batch 1 and
+// other grids too small to fill the chip; C, K <= 128 when forced): input
+// transform, the 64 Winograd-domain products and the output transform in ONE
+// launch, spread over many workgroups without any hand-off between them.
 //
 // The reference's fused kernel (/root/reference/csrc/nova_winograd_fused.hip:
 // 283-440, dispatched for every C, K <= 64 layer at :511) gives a workgroup 16
@@ -12,20 +12,23 @@
 // are B * ceil(P / T) * ceil(K / 16) independent workgroups (200 at conv2_x
 // batch 1), each on the latency chain of one kernel:
 //   * the wave's U fragments (fragment-ordered U, 16 output channels x the
-//     wave's positions x 2 channel chunks) are requested first and stay in flight
-//     during the transform;
+//     wave's positions x NKP 32-channel chunks) are requested first and stay
+//     in flight during the transform;
 //   * input transform, lane-parallel (8 lanes per patch, row pass, LDS
 //     transpose, column pass: the chains of input_lp_kernel, so V is
-//     bit-identical), 64 channels x NTH / 512 tiles per round; V goes to LDS as
+//     bit-identical), NTH / 8 patches per round; V goes to LDS as
 //     v_mfma_f32_16x16x32_f16 B operands with T tile slots (lanes of the
 //     empty slots read a zero block);
 //   * products: each of the NTH / 64 waves multiplies 64 / (NTH / 64)
-//     consecutive positions, one MFMA per position
-//     and 32-channel chunk, in the operand order of the fused tile-block
-//     kernel (so M is bit-identical to that kernel's);
+//     consecutive positions, one MFMA per position and 32-channel chunk, in
+//     the operand order of the fused tile-block kernel (so M is bit-identical
+//     to that kernel's);
 //   * M rounded to fp16 (the reference's rounding point,
 //     nova_winograd_fused.hip:405) to LDS, then the output transform,
 //     lane-parallel (the chains of output_lp_kernel) with the epilogue.
+// Above 64 input channels (NKP = 4) each workgroup reads 256 KB of U: at
+// ResNet-50 conv3_x batch 1 the launch takes 10.7 us against 9.9 us for the
+// three passes, so the automatic choice keeps it for C, K <= 64.
 #include <algorithm>
 #include <type_traits>
 
@@ -68,30 +71,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sm_rsrc(const void* p, int byt
 // 4*(l/16) .. +3 of both 16-channel halves) is 16 contiguous bytes.
 // Each position's block is padded by 8 halves (4 banks), so the 8 lanes of
 // a patch, which write 8 different positions, hit 8 different banks.
-template <int T>
+template <int T, int NKP>
 constexpr int sm_pos_halves() {
-    return 2 * 4 * T * 8 + 8;
+    return NKP * 4 * T * 8 + 8;
 }
-template <int T>
+template <int T, int NKP>
 __device__ __forceinline__ int sm_v_base(int pos, int chunk, int cg, int t) {
-    return pos * sm_pos_halves<T>() + ((chunk * 4 + cg) * T + t) * 8;
+    return pos * sm_pos_halves<T, NKP>() + ((chunk * 4 + cg) * T + t) * 8;
 }
-template <int T>
+template <int T, int NKP>
 __device__ __forceinline__ int sm_v_index(int pos, int c, int t) {
     const int chunk = c >> 5, cc = c & 31;
-    return sm_v_base<T>(pos, chunk, (cc >> 2) & 3, t) + ((cc >> 4) & 1) * 4 + (cc & 3);
+    return sm_v_base<T, NKP>(pos, chunk, (cc >> 2) & 3, t) + ((cc >> 4) & 1) * 4 + (cc & 3);
 }
 
-// NTH threads (512 or 1024): NTH / 512 tiles are transformed per round, each
-// wave multiplies 64 / (NTH / 64) positions.
-template <int T, int NTH, bool kNhwc, bool kEpi>
+// NTH threads (512 or 1024), NKP 32-channel chunks (input channels up to
+// 32 * NKP): the transform takes T * 32 * NKP patches of 8 lanes, NTH / 8
+// per round; each wave multiplies 64 / (NTH / 64) positions.
+template <int T, int NTH, int NKP, bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     constexpr int kWaves = NTH / 64;
     constexpr int kPpw = 64 / kWaves;                          // positions per wave
-    constexpr int kTpr = NTH / 512;                            // tiles per transform round
-    static_assert(T % kTpr == 0, "whole rounds");
-    constexpr int kVHalves = 64 * sm_pos_halves<T>();          // V of the group's tiles
-    constexpr int kTpFloats = 64 * kSmPitch * kTpr;            // one transpose buffer
+    constexpr int kCh = 32 * NKP;                              // channel slots
+    constexpr int kPatches = T * kCh;                          // patches of the group
+    constexpr int kPpr = NTH / 8;                              // patches per round
+    static_assert(kPatches % kPpr == 0, "whole rounds");
+    constexpr int kRounds = kPatches / kPpr;
+    constexpr int kVHalves = 64 * sm_pos_halves<T, NKP>();     // V of the group's tiles
+    constexpr int kTpFloats = kPpr * kSmPitch;                 // one transpose buffer
     __shared__ __align__(16) _Float16 vs[kVHalves + 8];        // + one zero block
     __shared__ __align__(16) float tps[2][kTpFloats];          // double-buffered transposes
     const int tid = threadIdx.x;
@@ -112,25 +119,25 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     const __amdgpu_buffer_rsrc_t yrs = sm_rsrc(a.y, a.y_bytes);
 
     // ---- 0. this wave's U operands: positions kPpw*w .. +kPpw-1, both chunks ----
-    h8 ua[kPpw][2];
+    h8 ua[kPpw][NKP];
 #pragma unroll
     for (int s = 0; s < kPpw; s++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NKP; j++) {
             const int pos = kPpw * wave + s;
             const int off = j < a.nkp ? ((pos * a.nkt + kb) * a.nkp + j) * 1024 : kSmOob;
             ua[s][j] = __builtin_bit_cast(
                 h8, __builtin_amdgcn_raw_buffer_load_b128(urs, lane * 16, off, 0));
         }
 
-    // ---- 1. input columns: lane (channel c, column j) of tile slot
-    // ts = tid / 512 in each round (kTpr slots per round), T / kTpr rounds ----
-    const int c = (tid >> 3) & 63, j = tid & 7, ts = tid >> 9;
-    constexpr int kRounds = T / kTpr;
+    // ---- 1. input columns: lane (patch pc = rd * kPpr + tid / 8, column j);
+    // patch pc is channel pc % kCh of tile slot pc / kCh ----
+    const int j = tid & 7;
     float d[kRounds][8];
 #pragma unroll
     for (int rd = 0; rd < kRounds; rd++) {
-        const int t = rd * kTpr + ts;
+        const int pc = rd * kPpr + (tid >> 3);
+        const int c = pc % kCh, t = pc / kCh;
         const int tl = t0 + min(t, ntiles - 1);
         const int th = tl / a.nw, tw = tl - (tl / a.nw) * a.nw;
         const int w = 6 * tw - a.pad + j;
@@ -149,10 +156,11 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     }
     if (tid < 2) *reinterpret_cast<unsigned long long*>(vs + kVHalves + 4 * tid) = 0ull;
 
-    // ---- 2. input transform, kTpr tiles per round (chains of input_lp_kernel) ----
+    // ---- 2. input transform, kPpr patches per round (chains of input_lp_kernel) ----
 #pragma unroll
     for (int rd = 0; rd < kRounds; rd++) {
-        const int t = rd * kTpr + ts;
+        const int pc = rd * kPpr + (tid >> 3);
+        const int c = pc % kCh, t = pc / kCh;
         float* tp = tps[rd & 1] + (tid >> 3) * kSmPitch;
 #pragma unroll
         for (int r = 0; r < 8; r++) {
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
 #pragma unroll
             for (int q = 0; q < 8; q++)
                 if (kBh[q][s2] != 0.0f) acc = __builtin_fmaf(tt[q], kBh[q][s2], acc);
-            vs[sm_v_index<T>(8 * j + s2, c, t)] = to_f16(acc);
+            vs[sm_v_index<T, NKP>(8 * j + s2, c, t)] = to_f16(acc);
         }
         // the next round writes the other transpose buffer; the one after
         // that reuses this one only after the next round's barrier
@@ -185,11 +193,11 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
 #pragma unroll
     for (int s = 0; s < kPpw; s++) acc[s] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int jc = 0; jc < 2; jc++)
+    for (int jc = 0; jc < NKP; jc++)
 #pragma unroll
         for (int s = 0; s < kPpw; s++) {
             const int pos = kPpw * wave + s;
-            const int vo = tl < T ? sm_v_base<T>(pos, jc, cg, tl) : kVHalves;
+            const int vo = tl < T ? sm_v_base<T, NKP>(pos, jc, cg, tl) : kVHalves;
             const h8 vb = *reinterpret_cast<const h8*>(vs + vo);
             acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[s][jc], vb, acc[s], 0, 0, 0);
         }
@@ -305,7 +313,8 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
 }  // namespace
 
 bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus, FusedSmallPlan* p) {
-    if (B < 1 || C < 1 || K < 1 || C > 64 || K > 64 || Cp > 64) return false;
+    if (B < 1 || C < 1 || K < 1 || C > 128 || K > 128 || Cp > 128) return false;
+    p->nkp = Cp <= 64 ? 2 : 4;
     const int P = nh * nw;
     // 2 tiles per workgroup: measured at conv2_x batch 1 (100 tiles), one
     // launch of 1, 2 or 4 tiles per workgroup took 8.3, 7.4 and 9.4 us (the
@@ -319,7 +328,9 @@ bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus, Fuse
     // (54 KB, two per CU) beyond. Measured, us, 1024 vs 512 threads:
     // conv2_x B=1 (200 workgroups) 7.5 vs 7.8, 32@56^2 B=2 (200) 6.9 vs 7.3,
     // 64@28^2 B=4 (208) 7.3 vs 7.8; conv2_x B=2 (400) 13.4 vs 10.4.
-    p->threads = p->grid <= (int64_t)cus ? 1024 : 512;
+    // More than 64 input channels: 1024 threads always (512 would hold
+    // 32 x 16 U fragment registers per thread).
+    p->threads = (p->grid <= (int64_t)cus || p->nkp == 4) ? 1024 : 512;
     return p->grid < ((int64_t)1 << 31);
 }
 
@@ -357,22 +368,25 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.relu = ep.relu;
     a.residual = reinterpret_cast<const _Float16*>(ep.residual);
     const dim3 grid((unsigned)p.grid), block((unsigned)p.threads);
-    if (p.tiles != 2 || (p.threads != 512 && p.threads != 1024))
+    if (p.tiles != 2 || (p.threads != 512 && p.threads != 1024) ||
+        (p.nkp != 2 && p.nkp != 4) || (p.nkp == 4 && p.threads != 1024) || Cp > 32 * p.nkp)
         return hipErrorInvalidConfiguration;
     auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
-    auto go_th = [&](auto nth) {
-        constexpr int N = decltype(nth)::value;
+    auto go_th = [&](auto nth, auto nkp) {
+        constexpr int N = decltype(nth)::value, NK = decltype(nkp)::value;
         if (epilogue_needed(ep.bias, ep.relu, ep.residual))
-            nhwc ? go(fused_small_kernel<2, N, true, true>)
-                 : go(fused_small_kernel<2, N, false, true>);
+            nhwc ? go(fused_small_kernel<2, N, NK, true, true>)
+                 : go(fused_small_kernel<2, N, NK, false, true>);
         else
-            nhwc ? go(fused_small_kernel<2, N, true, false>)
-                 : go(fused_small_kernel<2, N, false, false>);
+            nhwc ? go(fused_small_kernel<2, N, NK, true, false>)
+                 : go(fused_small_kernel<2, N, NK, false, false>);
     };
-    if (p.threads == 1024)
-        go_th(std::integral_constant<int, 1024>());
+    if (p.nkp == 4)
+        go_th(std::integral_constant<int, 1024>(), std::integral_constant<int, 4>());
+    else if (p.threads == 1024)
+        go_th(std::integral_constant<int, 1024>(), std::integral_constant<int, 2>());
     else
-        go_th(std::integral_constant<int, 512>());
+        go_th(std::integral_constant<int, 512>(), std::integral_constant<int, 2>());
     return hipGetLastError();
 }
 

@@ -158,6 +158,7 @@ struct FusedSmallPlan {
     int ntg;    // tile groups per image
     int nkb;    // 16-channel output blocks
     int threads;  // workgroup size: 512 or 1024
+    int nkp;      // 32-channel input chunks held in LDS: 2 (C <= 64) or 4 (C <= 128)
     int64_t grid;
 };
 bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus,

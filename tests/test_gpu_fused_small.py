@@ -1,10 +1,10 @@
-"""The small-problem fused kernel (path 5: one launch, kTiles tiles x 16
-output channels per workgroup, each workgroup recomputing its tiles' input
-transform) through the C-ABI.
+"""The small-problem fused kernel (path 5: one launch, 2 tiles x 16 output
+channels per workgroup, each workgroup recomputing its tiles' input
+transform; C, K <= 128) through the C-ABI.
 
 Its transforms are the lane-parallel chains and its products use the fused
 tile-block kernel's operand order, so wherever the tile-block kernel runs the
-result must equal it bit for bit; everywhere it must match the oracle within
+result must equal it bit for bit (C, K <= 64); everywhere it must match the oracle within
 the forward parity bar. Covered: batch 1 and small batches, C and K off the
 16/32 blocks (C = 3, 20, K = 8, 48), odd and non-square images, pads 0-2,
 channels-last, and the bias/residual/ReLU epilogue. A grid of at most one
@@ -57,6 +57,9 @@ CASES = [  # (B, C, K, H, W, pad)
     (4, 40, 24, 28, 28, 1),
     (1, 64, 64, 7, 7, 1),     # fewer tiles than a group (P = 4)
     (9, 24, 40, 30, 26, 0),   # 270 workgroups: the 512-thread variant, ragged K
+    (1, 128, 128, 28, 28, 1), # ResNet-50 conv3_x, batch 1: four 32-channel chunks
+    (2, 96, 72, 17, 23, 0),   # C, K between 64 and 128, off the 32-blocks
+    (3, 65, 128, 14, 14, 2),  # one channel past a 64-block, pad 2
 ]
 
 
@@ -83,7 +86,7 @@ def test_fused_small_matches_oracle_and_tile_block(oracle, B, C, K, H, W, pad):
 
 
 @pytest.mark.parametrize("B,C,K,H,pad", [(1, 64, 64, 56, 1), (2, 32, 48, 20, 1), (1, 16, 64, 13, 0),
-                                         (7, 32, 48, 28, 1)])
+                                         (7, 32, 48, 28, 1), (1, 128, 96, 28, 1)])
 def test_fused_small_channels_last_and_epilogue(B, C, K, H, pad):
     """NHWC in and out equals the NCHW result in the other memory format, bit
     for bit; bias/residual/ReLU equal the separate fp16 ops."""
@@ -106,12 +109,13 @@ def test_fused_small_channels_last_and_epilogue(B, C, K, H, pad):
     assert torch.equal(yce, ye)
 
 
-def test_fused_small_refused_above_64_channels():
+@pytest.mark.parametrize("C,K", [(160, 64), (64, 144)])
+def test_fused_small_refused_above_128_channels(C, K):
     from nova_winograd.ops import check
 
     torch.manual_seed(42)
-    x = torch.randn(1, 96, 14, 14, device=DEV).half()
-    w = torch.randn(64, 96, 3, 3, device=DEV) * 0.05
+    x = torch.randn(1, C, 14, 14, device=DEV).half()
+    w = torch.randn(K, C, 3, 3, device=DEV) * 0.05
     with pytest.raises(RuntimeError, match="fused path unsupported"):
         _run(x, w, 1, 5)
     check()
