@@ -371,28 +371,42 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
     return hipGetLastError();
 }
 
-// Kernel per shape: register-direct 64 x 16 for GEMV-like B=1 deep layers
-// (few tiles; two 16-row tiles per wave, which halves the V fragment loads
-// and doubles the U bytes each wave keeps in flight: 512@7^2 at batch 1
-// 7.1 -> 6.5 us, 1280@8^2 at batch 2 39.2 -> 34.9 us), LDS-tiled otherwise
-// -- 128 x 128 only for K >= 512 with many tiles, else 64 x 64, with two
-// channel stages in flight once there are 128 tiles or more. 8 waves per
-// workgroup except for 64 x 64 tiles at K > 256 below 128 tiles (whole
-// forwards, us, 4 -> 8 waves: 512@7^2 batch 32 27.2 -> 26.3 and batch 64
-// 34.7 -> 32.5; 128@28^2 batch 128 66.2 -> 63.1; 64@56^2 batch 1 10.6 ->
-// 10.4; but 1280@32^2 batch 1 52.5 -> 55.9). Measured on MI355X (kernel replay, us): ResNet-50 at batch
-// 32, 128@28^2 9.7 -> 9.3 and 256@14^2 11.2 -> 10.4 with 64 x 64 (two stages)
-// instead of 128 x 128; 512@7^2 at batch 128 31.3 (128 x 128) vs 39.2; the
-// second stage in flight costs 0.1-0.5 us below 128 tiles.
+// Kernel per shape. Register-direct 64 x 16 for GEMV-like batch-1 deep
+// layers (BP <= 16: few tiles; two 16-row tiles per wave, which halves the V
+// fragment loads and doubles the U bytes each wave keeps in flight: 512@7^2
+// at batch 1 7.1 -> 6.5 us, 1280@8^2 at batch 2 39.2 -> 34.9 us); LDS-tiled
+// otherwise, the tile chosen from a sweep of every tile shape on MI355X
+// (GEMM launch alone, per-kernel events, min of 2 x 60 launches, us; the
+// results are bit-identical across tile shapes):
+//  * 128 x 128 for K >= 512 with BP >= 256 (512@7^2 B=64 17.1 vs 20.3-22.4
+//    for the other shapes, B=128 31.4 vs 35.1-41.4);
+//  * 128 x 64 (8 waves) for K >= 1024 below 128 tiles (1280@16^2 B=2 33.6 vs
+//    36.4 for 64 x 64; 1280@32^2 B=1 34.0 vs 35.9; 640->1280@16^2 B=2 17.8 vs
+//    19.5);
+//  * 64 x 128, two stages in flight, for larger work: K >= 640 from 64 tiles,
+//    K >= 512 from 128, K >= 256 from 200, K <= 128 from 1600 (ResNet-50
+//    256@14^2 B=32 9.5 vs 11.0, B=128 24.6 vs 29.1; 512@7^2 B=32 10.8 vs
+//    11.2 for 128 x 128; 128@28^2 B=128 23.0 vs 26.0; SD-1.5 640@32^2 B=2
+//    14.4 vs 15.6, 320@64^2 B=2 8.8 vs 9.7; SDXL 640@64^2 14.5 vs 17.7;
+//    1280->640@32^2 B=2 23.6 vs 30.4);
+//  * else 64 x 64: two stages in flight from 128 tiles (128@28^2 B=32 8.7,
+//    128 x 128 8.7, 64 x 128 8.9; 256@14^2 B=16 7.5 vs 8.1 for 64 x 128),
+//    8 waves up to K = 256, 4 waves beyond (512@7^2 B=8 7.7 vs 8.0 with 8
+//    waves and 9.0 with 64 x 128; B=16 8.0 vs 9.3).
 static int wgemm_cfg(int K, int BP) {
     if (BP <= 16) return 0;
-    if (K >= 512 && BP >= 128) return 2;
+    if (K >= 512 && BP >= 256) return 2;
+    if (K >= 1024 && BP < 128) return 5;
+    if ((K >= 640 && BP >= 64) || (K >= 512 && BP >= 128) || (K >= 256 && BP >= 200) ||
+        (K <= 128 && BP >= 1600))
+        return 6;
     if (BP >= 128) return 3;
     return K <= 256 ? 4 : 1;
 }
 
 int wgemm_v_reads(int K, int BP) {
-    const int tk = wgemm_cfg(K, BP) == 2 ? 128 : 64;  // output channels per workgroup tile
+    const int cfg = wgemm_cfg(K, BP);
+    const int tk = (cfg == 2 || cfg == 5) ? 128 : 64;  // output channels per workgroup tile
     return (K + tk - 1) / tk;
 }
 
@@ -401,7 +415,9 @@ const char* wgemm_name(int K, int Cp, int BP) {
     static const char* names[] = {"wgemm_kernel<2, 1, 2, 1, 4>", "wgemm_lds_kernel<64, 64, 2, 2, 1>",
                                   "wgemm_lds_kernel<128, 128, 2, 4, 1>",
                                   "wgemm_lds_kernel<64, 64, 2, 4, 2>",
-                                  "wgemm_lds_kernel<64, 64, 2, 4, 1>"};
+                                  "wgemm_lds_kernel<64, 64, 2, 4, 1>",
+                                  "wgemm_lds_kernel<128, 64, 2, 4, 1>",
+                                  "wgemm_lds_kernel<64, 128, 2, 4, 2>"};
     return names[wgemm_cfg(K, BP)];
 }
 
@@ -412,6 +428,8 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
         case 1: return launch_lds<64, 64, 2, 2, 1>(U, V, M, K, Cp, BP, s);
         case 2: return launch_lds<128, 128, 2, 4, 1>(U, V, M, K, Cp, BP, s);
         case 3: return launch_lds<64, 64, 2, 4, 2>(U, V, M, K, Cp, BP, s);
+        case 5: return launch_lds<128, 64, 2, 4, 1>(U, V, M, K, Cp, BP, s);
+        case 6: return launch_lds<64, 128, 2, 4, 2>(U, V, M, K, Cp, BP, s);
         default: return launch_lds<64, 64, 2, 4, 1>(U, V, M, K, Cp, BP, s);
     }
 }

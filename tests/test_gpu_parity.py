@@ -122,18 +122,22 @@ def test_output_transform_bitexact(oracle, B, K, Ho, Wo):
     assert_same_bits(_u16(y), ref, "y")
 
 
-# Then: larger BP with K, Cp <= 128 (several bp tiles per position on the
-# 64 x 64 kernel with two stages in flight), partial 32-channel steps, K not a
-# multiple of 4; then K >= 512 with BP >= 128 (the 128 x 128 kernel), with a
-# partial k tile and a partial bp tile; last, K > 256 below 128 tiles (the
-# four-wave 64 x 64 kernel).
+# GEMM shapes by tile kernel (wgemm_cfg): BP <= 16 and small grids first
+# (register-direct and 64 x 64 kernels), larger BP with K, Cp <= 128 (several
+# bp tiles per position, two stages in flight), partial 32-channel steps, K not
+# a multiple of 4; K >= 512 from 128 tiles (64 x 128, with a partial k tile
+# and a partial bp tile), K > 256 below 128 tiles (the four-wave 64 x 64
+# kernel); then 64 x 128 at K <= 128 from 1600 tiles (16 x 64@56^2), K >= 256
+# from 200 and K >= 640 from 64, 128 x 128 at K >= 512 from 256 tiles, and
+# 128 x 64 at K >= 1024 below 128 tiles, each with partial tiles.
 GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256, 28),
               (1, 256, 256, 14), (1, 16, 40, 9), (8, 128, 128, 28), (2, 136, 200, 30),
               (4, 72, 132, 40),
               (16, 64, 64, 56), (12, 128, 128, 28), (12, 40, 24, 30), (12, 104, 100, 28),
               (12, 96, 98, 28),
               (32, 40, 520, 7), (33, 24, 516, 7),
-              (2, 64, 320, 14), (3, 48, 264, 20)]
+              (2, 64, 320, 14), (3, 48, 264, 20),
+              (8, 40, 264, 28), (2, 32, 648, 32), (66, 24, 516, 7), (1, 16, 1032, 28)]
 
 
 @pytest.mark.parametrize("B,C,K,H", GEMM_CASES)
