@@ -51,7 +51,8 @@ BATCHES = [1, 32]
 PEAK_HBM_GBS = 8000.0
 PEAK_FP16_TFLOPS = 2500.0
 KIND_NAMES = ["input", "gemm", "output", "fused"]
-PATH_NAMES = {1: "3-pass", 2: "fused_rows", 3: "fused_block", 4: "windowed", 5: "fused_small"}
+PATH_NAMES = {1: "3-pass", 2: "fused_rows", 3: "fused_block", 4: "windowed", 5: "fused_small",
+              6: "two_pass"}
 
 
 def log(*a):
@@ -70,16 +71,19 @@ def layer_roofline_us(B, C, K, H):
     return max(f_alg / (PEAK_FP16_TFLOPS * 1e12), b_alg / (PEAK_HBM_GBS * 1e9)) * 1e6
 
 
-def kernel_alg_bytes(kind, B, C, K, H):
+def kernel_alg_bytes(kind, B, C, K, H, name=""):
     """Algorithmic HBM bytes of one launch of a kernel kind (fp16 = 2 B):
     input transform reads x, writes V; GEMM reads U and V, writes M; output
-    transform reads M, writes y; fused reads x and U, writes y. Minimal
-    tiling P = ceil(Ho/6)^2, channel pitch C rounded up to 8."""
+    transform reads M, writes y; fused reads x and U, writes y -- except the
+    two-pass path's second kernel (gemm_out_kernel), which reads V and U and
+    writes y. Minimal tiling P = ceil(Ho/6)^2, channel pitch C rounded up to 8."""
     Cp = (C + 7) // 8 * 8
     Ho = H
     BP = B * (-(-Ho // 6)) ** 2
     x, y = 2 * B * C * H * H, 2 * B * K * Ho * Ho
     V, M, U = 2 * 64 * Cp * BP, 2 * 64 * K * BP, 2 * 64 * K * Cp
+    if kind == "fused" and name.startswith("gemm_out"):
+        return V + U + y
     return {"input": x + V, "gemm": U + V + M, "output": M + y, "fused": x + U + y}[kind]
 
 
@@ -184,8 +188,8 @@ KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_
 FAMILY_OF_KIND = {0: "input_transform_kernel", 1: "wgemm", 2: "output_transform_kernel"}
 
 NOVA_KERNELS = ["input_transform_kernel", "wgemm", "output_transform_kernel",
-                "fused_block_kernel", "fused_small_kernel", "fused_kernel<1>", "fused_kernel<2>",
-                "fused_kernel<4>"]
+                "fused_block_kernel", "fused_small_kernel", "gemm_out_kernel", "fused_kernel<1>",
+                "fused_kernel<2>", "fused_kernel<4>"]
 
 
 def _name_keys(name):
@@ -249,9 +253,8 @@ def mfma_from(pmc_dir, bench_json, out_path, cus=256):
                       "SQ_VALU_MFMA_BUSY_CYCLES / (bench avg_launch_us x "
                       f"{CLOCK_GHZ} GHz x {cus} CUs x 4 SIMDs)",
             "peak_tflops": PEAK_FP16_TFLOPS, "clock_ghz": CLOCK_GHZ, "kernels": []}
-    for name in ("wgemm", "fused_block_kernel", "fused_small_kernel", "fused_kernel<1>",
-                 "fused_kernel<2>",
-                 "fused_kernel<4>"):
+    for name in ("wgemm", "fused_block_kernel", "fused_small_kernel", "gemm_out_kernel",
+                 "fused_kernel<1>", "fused_kernel<2>", "fused_kernel<4>"):
         sel = {c: [r for r in per[c] if any(k in r[0] for k in _name_keys(name))]
                for c in MFMA_COUNTERS}
         mops = sel["SQ_INSTS_VALU_MFMA_MOPS_F16"]
@@ -870,7 +873,7 @@ def main():
                     lib.nova_get_last_error()  # kind not launched by this path
                     continue
                 ev = r["event"][k]
-                ab = kernel_alg_bytes(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"])
+                ab = kernel_alg_bytes(KIND_NAMES[k], r["B"], r["C"], r["K"], r["H"], kname)
                 r["kernels"][KIND_NAMES[k]] = {"kernel": kname, "avg_us": ev * 1e3,
                                               "replay_us": per * 1e3, "alg_bytes": ab,
                                               "gbs": ab / (ev * 1e-3) / 1e9}

@@ -135,7 +135,10 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
  * tile-block kernel (few channels, batch > 1), 5 = force the small-problem
  * fused kernel (C, K <= 128: one launch of 2 tiles x 16 output channels per
  * workgroup; chosen automatically for C, K <= 64 while its grid is at most
- * two workgroups per CU, e.g. batch 1), 4 = windowed 3-pass: the batch
+ * two workgroups per CU, e.g. batch 1), 6 = force the two-pass path (the
+ * input transform, then the 64 products and the output transform in one
+ * launch of 16 tiles x 32 output channels per workgroup, M kept on chip;
+ * bit-identical to 3-pass), 4 = windowed 3-pass: the batch
  * runs in windows of whole images whose V + M fit the window budget
  * (nova_set_window_bytes), each window's three kernels back to back -- the
  * BP-windowed pipeline of /root/reference/tests/test_bp_tiled.hip:482-571,
@@ -175,7 +178,8 @@ NOVA_API void nova_set_layout(nova_handle_t h, int nhwc);
 NOVA_API void nova_set_residual(nova_handle_t h, const void* d_residual_f16);
 /* Path the most recent forward on this handle took: 1 = 3-pass, 2 = fused
  * (position rows), 3 = fused (tile blocks), 4 = windowed 3-pass, 5 = fused
- * (small problems). */
+ * (small problems), 6 = two-pass (input transform + products with the output
+ * transform). */
 NOVA_API int nova_get_last_path(nova_handle_t h);
 
 /* No counterpart in the reference. nova_forward for callers that cannot

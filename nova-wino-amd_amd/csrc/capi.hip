@@ -105,6 +105,9 @@ struct Handle {
     uint16_t* Uf = nullptr;  // U in MFMA fragment order (fused kernels)
     size_t Uf_cap = 0;       // bytes
     bool uf_ready = false;   // Uf holds the current weights' fragments
+    uint16_t* Uw = nullptr;  // U in the two-pass kernel's block order (path 6)
+    size_t Uw_cap = 0;       // bytes
+    bool uw_ready = false;   // Uw holds the current weights' blocks
     void* ws = nullptr;
     size_t ws_cap = 0;  // bytes
     unsigned* cnt = nullptr;  // fused-kernel arrival counters, zero between launches
@@ -201,6 +204,31 @@ bool ensure_uf(Handle* H) {
     H->uf_ready = hip_ok(launch_u_frag(H->U, H->Uf, H->K, H->Cp, H->stream),
                          "filter fragment order");
     return H->uf_ready;
+}
+
+// The two-pass kernel's copy of U (launch_u_wfrag), built like Uf: at
+// set_weights when the automatic choice can pick path 6 or it is forced, else
+// on the first two-pass forward.
+bool ensure_uw(Handle* H) {
+    if (H->uw_ready) return true;
+    const size_t need = (size_t)u_frag_elems(H->K, H->Cp) * sizeof(uint16_t);
+    if ((int64_t)need >= ((int64_t)1 << 31)) {  // 32-bit offsets in the two-pass kernel
+        set_error(kErrInvalidArgument, "two-pass filter copy of %lld bytes exceeds 2^31 - 1",
+                  (long long)need);
+        return false;
+    }
+    if (need > H->Uw_cap) {
+        if (H->Uw) {
+            if (!hip_ok(hipFree(H->Uw), "hipFree(Uw)")) return false;
+            H->Uw = nullptr;
+            H->Uw_cap = 0;
+        }
+        if (!hip_ok(hipMalloc(&H->Uw, need), "hipMalloc(Uw)")) return false;
+        H->Uw_cap = need;
+    }
+    H->uw_ready = hip_ok(launch_u_wfrag(H->U, H->Uw, H->K, H->Cp, H->stream),
+                         "filter two-pass order");
+    return H->uw_ready;
 }
 
 // Counters of the fused kernel: zeroed once when (re)allocated; each launch
@@ -306,9 +334,31 @@ bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
     return fused_small_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, p);
 }
 
+// Layers the automatic choice may send to the two-pass path (their handles
+// build the two-pass copy of U with the weights).
+bool two_pass_possible(int C, int K) { return C <= 128 && K <= 128 && K >= C; }
+
+// Two-pass instead of three-pass (automatic choice), from MI355X forwards
+// (us, three-pass vs two-pass): 128@28^2 B=12 21.6 vs 19.6, B=24 26.9 vs
+// 24.1, B=32 27.1 vs 25.2; 96@28^2 B=16 20.4 vs 19.5, B=32 27.6 vs 21.6,
+// B=48 32.8 vs 24.2; 72@28^2 B=32 25.6 vs 19.9; 80->112@20^2 B=16 16.4 vs
+// 13.9; 64@56^2 B=8 21.3 vs 18.2. It loses with few workgroups (128@28^2
+// B=4 12.2 vs 16.8, B=8 17.2 vs 19.6), with a second round of them (128@28^2
+// B=64 37.3 vs 77.2; 128->256 B=32 34.5 vs 39.8), with K < C (128->64 B=32
+// 24.3 vs 26.5), and once the block-layout V passes ~15 MB (its 16-byte
+// pieces written from many workgroups: 128@28^2 B=40 29.6 vs 34.3, the input
+// transform 8.7 -> 15.8 us). Channels-last stays three-pass (not measured).
+bool two_pass_wins(const Handle* Hd, const Shape& s) {
+    if (Hd->nhwc || !two_pass_possible(Hd->C, Hd->K)) return false;
+    const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
+    const int64_t v_bytes = 2 * gemm_out_v_elems(Hd->Cp, s.BP);
+    return grid >= 64 && grid <= Hd->cus && v_bytes <= (int64_t)14 << 20;
+}
+
 int choose_path(const Handle* Hd, const Shape& s) {
     if (Hd->path_pref == 1) return 1;
     if (Hd->path_pref == 4) return 4;
+    if (Hd->path_pref == 6) return 6;
     if (Hd->path_pref == 5) {
         FusedSmallPlan p;
         return fused_small_plan_for(Hd, s, &p) ? 5 : 1;
@@ -355,7 +405,7 @@ int choose_path(const Handle* Hd, const Shape& s) {
         const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us
         if (t_fused < t_three) return 3;
     }
-    return 1;
+    return two_pass_wins(Hd, s) ? 6 : 1;
 }
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
@@ -396,6 +446,46 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
     const bool ok_out = hip_ok(out(), "output transform");
     pf.done(kKindOutput, e, "output_transform_kernel");
     return ok_out;
+}
+
+// Two-pass forward on one sub-batch (path 6): the three-pass input transform
+// into V, then the products and the output transform in one launch (M stays
+// on chip). Same V, M and y as run_three_pass, bit for bit.
+bool run_two_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* V,
+                  bool remember, const Epilogue& ep) {
+    Profiler& pf = Hd->prof;
+    const hipStream_t st = Hd->stream;
+    const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+    const uint16_t* U = Hd->Uw;
+    const bool nhwc = Hd->nhwc != 0;
+    // V in the two-pass block layout: the 16-byte pieces of a line come from
+    // up to 8 workgroups, so V goes through the L2, where they merge (streamed
+    // past it, the partial lines reach memory one by one: conv3_x batch 32,
+    // cache-cold forward 35.9 -> 47.9 us)
+    const bool stream_v = false;
+    const int vfrag = (Cp + 31) / 32;
+    const int64_t pstride = gemm_out_v_elems(Cp, s.BP) / 64;
+    auto in = [=]() {
+        return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp, pstride, st,
+                                      nhwc, stream_v, vfrag);
+    };
+    auto go = [=]() {
+        return launch_gemm_out(U, V, y, s.B, K, Cp, s.nh, s.nw, s.Ho, s.Wo, st, ep, nhwc);
+    };
+    if (remember) {
+        pf.last[kKindInput] = in;
+        pf.last[kKindGemm] = nullptr;
+        pf.last[kKindOutput] = nullptr;
+        pf.last[kKindFused] = go;
+    }
+    size_t e = pf.arm();
+    const bool ok_in = hip_ok(in(), "input transform");
+    pf.done(kKindInput, e, "input_transform_kernel");
+    if (!ok_in) return false;
+    e = pf.arm();
+    const bool ok_go = hip_ok(go(), "products + output transform");
+    pf.done(kKindFused, e, "gemm_out_kernel");
+    return ok_go;
 }
 
 // ---- scratch of the allocation-free forward (nova_forward_noalloc) -------
@@ -462,7 +552,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     if (no_alloc) {
         // the position-row kernel needs an allocated M buffer and counters,
         // and a fragment copy not yet built would be allocated here
-        if (path == 2 || ((path == 3 || path == 5) && !Hd->uf_ready)) path = 1;
+        if (path == 2 || path == 6 || ((path == 3 || path == 5) && !Hd->uf_ready)) path = 1;
         const int64_t per_img = 2 * (int64_t)64 * (Hd->Cp + Hd->K) * s_all.nh * s_all.nw;
         if ((path == 1 || path == 4) && per_img > (int64_t)NOVA_NOALLOC_SCRATCH_BYTES - 256) {
             set_error(kErrWorkspace,
@@ -477,6 +567,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     }
     const bool fused = path == 2 || path == 3 || path == 5;
     if (fused && !ensure_uf(Hd)) return;
+    if (path == 6 && !ensure_uw(Hd)) return;
     if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3 || Hd->path_pref == 5)) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
@@ -485,7 +576,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     // workspace for the largest sub-batch
     const int64_t Bc = std::min<int64_t>(chunk, s_all.B);
     const int64_t BPc = Bc * s_all.nh * s_all.nw;
-    const int64_t needV = 64 * (int64_t)Hd->Cp * BPc;
+    const int64_t needV = path == 6 ? gemm_out_v_elems(Hd->Cp, BPc) : 64 * (int64_t)Hd->Cp * BPc;
     const int64_t needM = 64 * (int64_t)Hd->K * BPc;
     uint16_t* V = nullptr;
     uint16_t* M = nullptr;
@@ -495,7 +586,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     } else if (!fused) {
         size_t ws_bytes = 0;
         const bool userV = V_user && needV <= V_cap && aligned16(V_user);
-        const bool userM = M_user && needM <= M_cap && aligned16(M_user);
+        const bool userM = path == 6 || (M_user && needM <= M_cap && aligned16(M_user));
         if (!userV) ws_bytes += (size_t)needV * 2;
         if (!userM) ws_bytes += (size_t)needM * 2;
         if (ws_bytes && !ensure_ws(Hd, ws_bytes)) return;
@@ -506,7 +597,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             V = reinterpret_cast<uint16_t*>(wsp);
             wsp += (size_t)needV * 2;
         }
-        M = userM ? static_cast<uint16_t*>(M_user) : reinterpret_cast<uint16_t*>(wsp);
+        M = path == 6 ? nullptr
+                      : userM ? static_cast<uint16_t*>(M_user) : reinterpret_cast<uint16_t*>(wsp);
     }
 
     Profiler& pf = Hd->prof;
@@ -589,6 +681,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             const bool ok = hip_ok(fz(), "fused kernel");
             pf.done(kKindFused, e0, fused_name(fp));
             if (!ok) return;
+        } else if (path == 6) {
+            if (!run_two_pass(Hd, xx, yy, s, V, b0 == 0, ep)) return;
         } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0 && !no_alloc, ep, !no_alloc)) {
             return;
         }
@@ -614,6 +708,7 @@ void nova_destroy(nova_handle_t h) {
     if (!H) return;
     if (H->U) hip_ok(hipFree(H->U), "hipFree(U)");
     if (H->Uf) hip_ok(hipFree(H->Uf), "hipFree(Uf)");
+    if (H->Uw) hip_ok(hipFree(H->Uw), "hipFree(Uw)");
     if (H->ws) hip_ok(hipFree(H->ws), "hipFree(workspace)");
     if (H->cnt) hip_ok(hipFree(H->cnt), "hipFree(counters)");
     for (hipEvent_t e : H->prof.pool) (void)hipEventDestroy(e);
@@ -661,6 +756,7 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
         H->U_cap = need;
     }
     H->uf_ready = false;
+    H->uw_ready = false;
     H->K = K;
     H->C = C;
     H->Cp = Cp;
@@ -677,6 +773,8 @@ void set_weights_impl(nova_handle_t h, const void* d_weight, int K, int C, bool 
     const bool fused_possible = (C <= 64 && K <= 64 && H->path_pref == 0) ||
                                 H->path_pref == 2 || H->path_pref == 3 || H->path_pref == 5;
     if (H->ready && fused_possible) H->ready = ensure_uf(H);
+    if (H->ready && (H->path_pref == 6 || (H->path_pref == 0 && two_pass_possible(C, K))))
+        H->ready = ensure_uw(H);
 }
 
 }  // namespace
@@ -884,13 +982,14 @@ void nova_set_stream(nova_handle_t h, void* stream) {
 void nova_set_path(nova_handle_t h, int path) {
     Handle* H = as_handle(h, "nova_set_path");
     if (!H) return;
-    if (path < 0 || path > 5) {
-        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2, 3, 4 or 5");
+    if (path < 0 || path > 6) {
+        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2, 3, 4, 5 or 6");
         return;
     }
     H->path_pref = path;
     if ((path == 2 || path == 3 || path == 5) && H->ready)
         ensure_uf(H);  // fused forced after the weights
+    if (path == 6 && H->ready) ensure_uw(H);
 }
 
 void nova_set_window_bytes(nova_handle_t h, long long bytes) {
@@ -945,6 +1044,7 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     int64_t chunk = std::max<int64_t>(1, batch_chunk(Hd, s));
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s));
     const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;
+    if (path == 6) return (long long)(gemm_out_v_elems(Hd->Cp, BPc) * 2);  // V only
     return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * BPc * 2);
 }
 

@@ -82,15 +82,22 @@ inline int64_t u_frag_elems(int K, int Cp) {
     return (int64_t)64 * ((K + 15) / 16) * ((Cp + 31) / 32) * 512;
 }
 hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStream_t s);
+// The two-pass kernel's U blocks (three-pass GEMM lane layout, contiguous;
+// same size as the fused kernels' copy).
+hipError_t launch_u_wfrag(const uint16_t* U, uint16_t* Uw, int K, int Cp, hipStream_t s);
 
 // ---- input transform -----------------------------------------------------
 // V[p*pstride + bp*ldv + c], bp = (b*nh + th)*nw + tw, for th < nh, tw < nw.
 // Channels c in [C, ldv) are written as zero. x is NCHW, or NHWC if nhwc.
 // stream_v: the tile-block forms store V with the non-temporal (nt) cache
 // policy (results unchanged; see wgemm_v_reads for when it pays).
+// vfrag: 0 = V in the product layout V[p][bp][ldv]; otherwise the number of
+// 32-channel chunks of the two-pass layout (1 KB MFMA B-operand blocks of 16
+// tiles x 32 channels; pstride = ceil(BP / 16) * vfrag * 512 halves).
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s, bool nhwc = false, bool stream_v = false);
+                                  hipStream_t s, bool nhwc = false, bool stream_v = false,
+                                  int vfrag = 0);
 
 // ---- output transform ----------------------------------------------------
 // Reads M[p*pstride + bp*ldm + k]; writes y[b][k][h][w] (y[b][h][w][k] if
@@ -167,6 +174,16 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
                               int Wo, const FusedSmallPlan& p, hipStream_t s,
                               Epilogue ep = Epilogue(), bool nhwc = false);
+
+// Two-pass forward, second pass (path 6): the products and the output
+// transform of 16 tiles x 32 output channels per workgroup, U from the
+// launch_u_wfrag blocks and V in the two-pass layout (launch_input_transform
+// with vfrag = ceil(Cp / 32)); M stays in LDS.
+int64_t gemm_out_grid(int K, int BP);
+int64_t gemm_out_v_elems(int Cp, int64_t BP);  // V halves of the two-pass layout
+hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, int B, int K,
+                           int Cp, int nh, int nw, int Ho, int Wo, hipStream_t s, Epilogue ep,
+                           bool nhwc);
 
 // ---- weight gradient (Winograd domain, fp32) --------------------------------
 // Plan of a weight-gradient computation: images per sub-batch (the fp32

@@ -117,6 +117,37 @@ hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStre
     return hipGetLastError();
 }
 
+// Reorder U[p][k][Cp] into the two-pass kernel's A-operand blocks: per
+// (position, 16-row tile, 32-channel chunk) 1 KB in which lane l holds row
+// l % 16 and channels 8*(l/16) .. +7 -- the three-pass GEMM's lane layout,
+// stored contiguously (zero padded). One thread per lane slot.
+__global__ __launch_bounds__(256) void u_wfrag_kernel(const _Float16* __restrict__ U,
+                                                       _Float16* __restrict__ Uw, int K, int Cp,
+                                                       int nkt, int nkp, int64_t nslots) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nslots) return;
+    const int lane = (int)(i & 63);
+    const int64_t frag = i >> 6;  // (p*nkt + kt)*nkp + j
+    const int j = (int)(frag % nkp);
+    const int kt = (int)((frag / nkp) % nkt);
+    const int p = (int)(frag / ((int64_t)nkp * nkt));
+    const int k = kt * 16 + (lane & 15);
+    const int c = j * 32 + 8 * (lane >> 4);
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 v = {};
+    if (k < K && c < Cp) v = *reinterpret_cast<const h8*>(U + ((int64_t)p * K + k) * Cp + c);
+    *reinterpret_cast<h8*>(Uw + i * 8) = v;
+}
+
+hipError_t launch_u_wfrag(const uint16_t* U, uint16_t* Uw, int K, int Cp, hipStream_t s) {
+    const int nkt = (K + 15) / 16, nkp = (Cp + 31) / 32;
+    const int64_t nslots = (int64_t)64 * nkt * nkp * 64;
+    launch(u_wfrag_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), s,
+        reinterpret_cast<const _Float16*>(U), reinterpret_cast<_Float16*>(Uw), K, Cp, nkt, nkp,
+        nslots);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Buffer-resource helpers. Every tensor is addressed through a raw buffer
 // resource: an offset at or past num_records reads 0 and drops stores, so
@@ -135,6 +166,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
                                              (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
                                              0x00020000);
+}
+
+// Byte offset of V element (tile bp, channel c) within one position's plane.
+// vfrag == 0: the product layout [bp][ldv]. vfrag = number of 32-channel
+// chunks: the two-pass layout, 1 KB blocks (bp / 16, c / 32) in which lane
+// (bp % 16) + 16 * ((c % 32) / 8) holds 8 consecutive channels -- the B
+// operand of v_mfma_f32_16x16x32_f16 for 16 tiles, one contiguous 1 KB load
+// per wave.
+__device__ __forceinline__ int v_plane_off(int bp, int c, int ldv, int vfrag) {
+    if (vfrag == 0) return 2 * (bp * ldv + c);
+    return ((bp >> 4) * vfrag + (c >> 5)) * 1024 + ((bp & 15) + 16 * ((c & 31) >> 3)) * 16 +
+           (c & 7) * 2;
 }
 
 // ---------------------------------------------------------------------------
@@ -173,7 +216,7 @@ template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int xd,
-    int64_t v_bytes) {
+    int64_t v_bytes, int vfrag) {
     using G = InGeom<TW>;
     __shared__ __align__(16) unsigned char sx[G::kBytes];
     // 1-D grid over (tile block, tile row, image x channel block), x fastest
@@ -237,7 +280,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     const int tw = tw0 + t;
     const int c = c0 + cc;
     const int bp = (b * nh + th) * nw + tw;
-    const int voff = (tw < nw && c < ldv) ? 2 * (bp * ldv + c) : kOob;
+    const int voff = (tw < nw && c < ldv) ? v_plane_off(bp, c, ldv, vfrag) : kOob;
     unsigned cmask = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -303,7 +346,8 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
 template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_nhwc_kernel(
     const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
-    int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int64_t v_bytes) {
+    int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int64_t v_bytes,
+    int vfrag) {
     constexpr int kCB = 256 / TW;
     constexpr int kCols = 6 * TW + 2;
     constexpr int kPix = kCB + 8;            // halves per staged pixel
@@ -345,7 +389,7 @@ __global__ __launch_bounds__(256) void input_nhwc_kernel(
     const int tw = tw0 + t;
     const int c = c0 + cc;
     const int bp = (b * nh + th) * nw + tw;
-    const int voff = (tw < nw && c < ldv) ? 2 * (bp * ldv + c) : kOob;
+    const int voff = (tw < nw && c < ldv) ? v_plane_off(bp, c, ldv, vfrag) : kOob;
     const _Float16* src = sx + 6 * t * kPix + cc;
     input_tile_rows([&](int i, int j) { return (float)src[(i * kCols + j) * kPix]; },
                     [&](int r, int s2, float v) {
@@ -378,7 +422,7 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
                                                        _Float16* __restrict__ V, int C, int H,
                                                        int W, int pad, int nh, int nw, int ldv,
                                                        int64_t pstride, int ncg, int x_bytes,
-                                                       int64_t v_bytes) {
+                                                       int64_t v_bytes, int vfrag) {
     __shared__ float tls[4 * 8 * kLpPitch];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
@@ -419,7 +463,7 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
     float t[8];
 #pragma unroll
     for (int q = 0; q < 8; q++) t[q] = tp[j * 8 + q];
-    const int voff = c < ldv ? 2 * (int)(8 * j * pstride + (int64_t)bp * ldv + c) : kOob;
+    const int voff = c < ldv ? 2 * (int)(8 * j * pstride) + v_plane_off(bp, c, ldv, vfrag) : kOob;
 #pragma unroll
     for (int s = 0; s < 8; s++) {
         float acc = 0.0f;
@@ -433,7 +477,7 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
 
 static hipError_t launch_input_lp(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s, bool nhwc) {
+                                  hipStream_t s, bool nhwc, int vfrag) {
     const int ncg = (ldv + 31) / 32;
     const int64_t items = (int64_t)B * nh * nw * ncg;
     if (items >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
@@ -442,11 +486,11 @@ static hipError_t launch_input_lp(const uint16_t* x, uint16_t* V, int B, int C, 
     if (nhwc)
         launch(input_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
-            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
+            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
     else
         launch(input_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
-            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride);
+            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
     return hipGetLastError();
 }
 
@@ -491,10 +535,10 @@ static bool latency_bound(int64_t rows, int n, int ch) {
 
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
-                                  hipStream_t s, bool nhwc, bool stream_v) {
+                                  hipStream_t s, bool nhwc, bool stream_v, int vfrag) {
     if (latency_bound((int64_t)B * nh, nw, ldv) ||
         (nhwc && (C % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0)))
-        return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, nhwc);
+        return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, nhwc, vfrag);
     const int tw = pick_tw((int64_t)B * nh, nw, ldv);
     const int cb = 256 / tw;
     const int cblocks = (ldv + cb - 1) / cb;
@@ -508,7 +552,7 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
         const _Float16* xh = reinterpret_cast<const _Float16*>(x);
         auto go = [&](auto kernel) {
             launch(kernel, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
-                   (int)x_bytes, 2 * 64 * pstride);
+                   (int)x_bytes, 2 * 64 * pstride, vfrag);
         };
         if (tw == 2)
             stream_v ? go(input_nhwc_kernel<2, true>) : go(input_nhwc_kernel<2, false>);
@@ -527,7 +571,7 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
     auto go = [&](auto kernel) {
         launch(kernel, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
-               (int)x_bytes, xd, 2 * 64 * pstride);
+               (int)x_bytes, xd, 2 * 64 * pstride, vfrag);
     };
     if (tw == 2)
         stream_v ? go(input_transform_kernel<2, true>) : go(input_transform_kernel<2, false>);

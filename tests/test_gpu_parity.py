@@ -227,7 +227,8 @@ def _forward_case(oracle, B, C, K, H, W, pad, path):
     return yg, yo, truth, took
 
 
-@pytest.mark.parametrize("path", [1, 2, 3], ids=["3pass", "fused_rows", "fused_block"])
+@pytest.mark.parametrize("path", [1, 2, 3, 6], ids=["3pass", "fused_rows", "fused_block",
+                                                     "two_pass"])
 @pytest.mark.parametrize("B,C,K,H,W,pad", FORWARD_CASES)
 def test_forward_matches_oracle(oracle, B, C, K, H, W, pad, path):
     print(f"[forward] B={B} C={C} K={K} H={H} W={W} pad={pad} path={path}", flush=True)

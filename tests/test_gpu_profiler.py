@@ -17,7 +17,7 @@ DEV = torch.device("cuda:0")
 
 
 @pytest.mark.parametrize("path,B,C,K,H", [(1, 2, 64, 64, 28), (3, 32, 64, 64, 56),
-                                          (1, 4, 128, 96, 14)])
+                                          (1, 4, 128, 96, 14), (6, 4, 128, 96, 14)])
 def test_profile_counts_and_intervals(path, B, C, K, H):
     from nova_winograd.ops import check, get_lib
 
@@ -50,7 +50,7 @@ def test_profile_counts_and_intervals(path, B, C, K, H):
         timed = lib.nova_profile_read(h, tot, cnt)
         check()
         assert torch.equal(y0, y1)
-        kinds = [0, 1, 2] if path == 1 else [3]
+        kinds = {1: [0, 1, 2], 6: [0, 3]}.get(path, [3])
         assert timed == n * len(kinds)
         for k in range(4):
             if k in kinds:
@@ -72,7 +72,8 @@ def test_profile_counts_and_intervals(path, B, C, K, H):
         lib.nova_destroy(h)
 
 
-@pytest.mark.parametrize("path,B,C,K,H", [(1, 2, 64, 64, 28), (3, 32, 64, 64, 56)])
+@pytest.mark.parametrize("path,B,C,K,H", [(1, 2, 64, 64, 28), (3, 32, 64, 64, 56),
+                                          (6, 3, 96, 128, 28)])
 def test_profile_replay(path, B, C, K, H):
     """nova_profile_replay re-launches the last forward's kernels (they are
     idempotent: the output is unchanged), returns a positive mean time for
@@ -93,7 +94,7 @@ def test_profile_replay(path, B, C, K, H):
         check()
         torch.cuda.synchronize()
         y0 = y.clone()
-        kinds = [0, 1, 2] if path == 1 else [3]
+        kinds = {1: [0, 1, 2], 6: [0, 3]}.get(path, [3])
         for k in range(4):
             ms = lib.nova_profile_replay(h, k, 5)
             if k in kinds:
