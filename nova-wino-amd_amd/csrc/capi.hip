@@ -336,23 +336,24 @@ bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
 
 // Layers the automatic choice may send to the two-pass path (their handles
 // build the two-pass copy of U with the weights).
-bool two_pass_possible(int C, int K) { return C <= 128 && K <= 128 && K >= C; }
+bool two_pass_possible(int C, int K) { return C <= 128 && K <= 128 && 2 * K >= C; }
 
 // Two-pass instead of three-pass (automatic choice), from MI355X forwards
-// (us, three-pass vs two-pass): 128@28^2 B=12 21.6 vs 19.6, B=24 26.9 vs
-// 24.1, B=32 27.1 vs 25.2; 96@28^2 B=16 20.4 vs 19.5, B=32 27.6 vs 21.6,
-// B=48 32.8 vs 24.2; 72@28^2 B=32 25.6 vs 19.9; 80->112@20^2 B=16 16.4 vs
-// 13.9; 64@56^2 B=8 21.3 vs 18.2. It loses with few workgroups (128@28^2
-// B=4 12.2 vs 16.8, B=8 17.2 vs 19.6), with a second round of them (128@28^2
-// B=64 37.3 vs 77.2; 128->256 B=32 34.5 vs 39.8), with K < C (128->64 B=32
-// 24.3 vs 26.5), and once the block-layout V passes ~15 MB (its 16-byte
-// pieces written from many workgroups: 128@28^2 B=40 29.6 vs 34.3, the input
-// transform 8.7 -> 15.8 us). Channels-last stays three-pass (not measured).
+// (us, three-pass vs two-pass, warm / cache-cold): 128@28^2 B=24 26.7 / 32.7
+// vs 22.4 / 31.2, B=32 27.8 / 35.3 vs 24.1 / 32.3, B=40 30.0 / 40.9 vs 26.8 /
+// 36.8; 96@28^2 B=32 26.7 / 32.9 vs 20.2 / 28.0, B=48 32.5 / 40.6 vs 23.8 /
+// 33.0; 72@28^2 B=32 25.4 / 30.5 vs 18.9 / 25.8; 64@56^2 B=8 21.5 / 26.4 vs
+// 16.7 / 23.3; 128->64@28^2 B=32 24.1 / 31.4 vs 22.6 / 31.0; 48->40@13^2
+// B=128 23.0 / 30.9 vs 17.3 / 23.0; 64->48@28^2 B=64 29.1 / 34.7 vs 21.5 /
+// 28.4; 128@112^2 B=1 24.2 / 28.9 vs 20.7 / 29.4. It loses with
+// few workgroups (128@28^2 B=4 12.3 vs 16.8, B=8 17.5 vs 19.7) and with a
+// second round of them (128@28^2 B=64 36.7 vs 41.5; 128->256 B=32 34.9 vs
+// 39.9). Channels-last stays three-pass (not measured).
 bool two_pass_wins(const Handle* Hd, const Shape& s) {
     if (Hd->nhwc || !two_pass_possible(Hd->C, Hd->K)) return false;
     const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
     const int64_t v_bytes = 2 * gemm_out_v_elems(Hd->Cp, s.BP);
-    return grid >= 64 && grid <= Hd->cus && v_bytes <= (int64_t)14 << 20;
+    return grid >= 64 && grid <= Hd->cus && v_bytes <= (int64_t)20 << 20;
 }
 
 int choose_path(const Handle* Hd, const Shape& s) {

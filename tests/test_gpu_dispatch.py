@@ -66,12 +66,14 @@ AUTO_CASES = [
     (128, 64, 64, 56, 3),  # four waves
     (16, 64, 64, 56, 3),   # 112 workgroups, one wave: 23 vs 23.1 us
     (8, 64, 64, 56, 6),    # 56 workgroups: 23 vs 16.5 us (small kernel: 1600 workgroups);
-                           # two-pass (100 workgroups) 18.2 vs three-pass 21.3 us
+                           # two-pass (100 workgroups) 16.7 vs three-pass 21.5 us
     (8, 32, 32, 56, 3),    # one 32-channel chunk: 13 vs 16 us
-    (128, 48, 40, 13, 1),  # small images: 23 vs 16 us
-    (32, 128, 128, 28, 6),  # conv3_x: more than 64 channels, two-pass 25.2 vs 27.1 us
-    (40, 128, 128, 28, 1),  # two-pass V past 14 MB: three-pass
-    (32, 128, 64, 28, 1),   # K < C: three-pass
+    (128, 48, 40, 13, 6),  # small images: fused 23 vs 16 us; two-pass 17.3 vs three-pass 23.0
+    (32, 128, 128, 28, 6),  # conv3_x: more than 64 channels, two-pass 24.1 vs 27.8 us
+    (40, 128, 128, 28, 6),  # 252 workgroups: two-pass 26.8 vs 30.0 us
+    (64, 128, 128, 28, 1),  # 400 workgroups (a second round): three-pass 36.7 vs 41.5 us
+    (32, 128, 64, 28, 6),   # K = C / 2: two-pass 22.6 vs 24.1 us
+    (32, 128, 32, 28, 1),   # K < C / 2: three-pass
     (1, 64, 64, 56, 5),    # B=1: the small-problem kernel (200 workgroups)
     (2, 64, 64, 56, 5),    # 400 workgroups
     (4, 64, 64, 56, 1),    # 800 workgroups: three-pass
