@@ -348,9 +348,11 @@ bool two_pass_possible(int C, int K) { return C <= 128 && K <= 128 && 2 * K >= C
 // 28.4; 128@112^2 B=1 24.2 / 28.9 vs 20.7 / 29.4. It loses with
 // few workgroups (128@28^2 B=4 12.3 vs 16.8, B=8 17.5 vs 19.7) and with a
 // second round of them (128@28^2 B=64 36.7 vs 41.5; 128->256 B=32 34.9 vs
-// 39.9). Channels-last stays three-pass (not measured).
+// 39.9). Channels-last the same (128@28^2 B=32 26.6 / 36.3 vs 23.7 / 31.5;
+// 96@28^2 B=32 26.1 / 31.9 vs 19.1 / 26.8; 48->40@13^2 B=128 22.1 / 27.6 vs
+// 16.8 / 22.0).
 bool two_pass_wins(const Handle* Hd, const Shape& s) {
-    if (Hd->nhwc || !two_pass_possible(Hd->C, Hd->K)) return false;
+    if (!two_pass_possible(Hd->C, Hd->K)) return false;
     const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
     const int64_t v_bytes = 2 * gemm_out_v_elems(Hd->Cp, s.BP);
     return grid >= 64 && grid <= Hd->cus && v_bytes <= (int64_t)20 << 20;

@@ -62,7 +62,8 @@ def test_nhwc_equals_nchw(B, C, K, H, pad):
     x = torch.randn(B, C, H, H, device=DEV).half()
     w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
     y, took = _run(x.contiguous(memory_format=CL), w, pad, True)
-    assert took in (1, 5)  # three-pass, or the small-problem kernel for small grids
+    assert took in (1, 5, 6)  # three-pass, the small-problem kernel for small grids, or
+    #                            two-pass (conv3_x at batch 32, conv2_x at batch 8)
     y_ref, took_ref = _run(x, w, pad, False, path=took)  # the same path in NCHW
     assert took_ref == took
     assert y.is_contiguous(memory_format=CL)
