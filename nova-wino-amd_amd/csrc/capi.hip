@@ -406,7 +406,20 @@ int choose_path(const Handle* Hd, const Shape& s) {
         const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
                            4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
         const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us
-        if (t_fused < t_three) return 3;
+        // The two-pass path beats the tile-block kernel from two 32-channel
+        // chunks up while its grid leaves a fifth of the CUs free (us,
+        // tile-block vs two-pass, NCHW / NHWC: 64@56^2 B=12 23.5 vs 18.8 /
+        // 24.6 vs 19.0, B=16 23.6 vs 19.9 / 25.0 vs 20.0; 64@28^2 B=48 23.1 vs
+        // 19.2 / 24.0 vs 18.6; 48@56^2 B=16 22.1 vs 18.0 / 24.7 vs 18.3;
+        // 64->48@28^2 B=32 22.0 vs 18.4 / 23.7 vs 17.6); not at one chunk
+        // (32@56^2 B=32 15.2 vs 18.5), and by little or not at all nearer a
+        // full round (250 workgroups: 64@56^2 B=20 23.8 vs 23.3, cold 29.8 vs
+        // 32.4; 64@28^2 B=80 23.8 vs 25.1).
+        if (t_fused < t_three) {
+            const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
+            const bool two = Hd->Cp > 32 && 5 * grid <= 4 * (int64_t)Hd->cus && two_pass_wins(Hd, s);
+            return two ? 6 : 3;
+        }
     }
     return two_pass_wins(Hd, s) ? 6 : 1;
 }

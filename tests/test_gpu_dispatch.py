@@ -64,7 +64,10 @@ AUTO_CASES = [
     (48, 64, 64, 56, 3),   # two waves, 46 vs 49 us (measured 50.5 vs 49.1: a near miss)
     (64, 64, 64, 56, 3),   # two waves, 46 vs 62 us
     (128, 64, 64, 56, 3),  # four waves
-    (16, 64, 64, 56, 3),   # 112 workgroups, one wave: 23 vs 23.1 us
+    (16, 64, 64, 56, 6),   # two-pass (200 workgroups, one round) 20.0 vs tile-block 23.6 us
+    (48, 64, 64, 28, 6),   # two-pass 19.2 vs tile-block 23.1 us
+    (80, 64, 64, 28, 3),   # 250 workgroups: tile-block 23.8 vs two-pass 25.1 us
+    (32, 32, 32, 56, 3),   # one 32-channel chunk: tile-block 15.2 vs two-pass 18.5 us
     (8, 64, 64, 56, 6),    # 56 workgroups: 23 vs 16.5 us (small kernel: 1600 workgroups);
                            # two-pass (100 workgroups) 16.7 vs three-pass 21.5 us
     (8, 32, 32, 56, 3),    # one 32-channel chunk: 13 vs 16 us
