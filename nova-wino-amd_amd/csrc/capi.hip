@@ -336,7 +336,7 @@ bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
 
 // Layers the automatic choice may send to the two-pass path (their handles
 // build the two-pass copy of U with the weights).
-bool two_pass_possible(int C, int K) { return C <= 128 && K <= 128 && 2 * K >= C; }
+bool two_pass_possible(int C, int K) { return C <= 128 && K <= 256 && 2 * K >= C; }
 
 // Two-pass instead of three-pass (automatic choice), from MI355X forwards
 // (us, three-pass vs two-pass, warm / cache-cold): 128@28^2 B=24 26.7 / 32.7
@@ -350,12 +350,21 @@ bool two_pass_possible(int C, int K) { return C <= 128 && K <= 128 && 2 * K >= C
 // second round of them (128@28^2 B=64 36.7 vs 41.5; 128->256 B=32 34.9 vs
 // 39.9). Channels-last the same (128@28^2 B=32 26.6 / 36.3 vs 23.7 / 31.5;
 // 96@28^2 B=32 26.1 / 31.9 vs 19.1 / 26.8; 48->40@13^2 B=128 22.1 / 27.6 vs
-// 16.8 / 22.0).
+// 16.8 / 22.0). Above 128 output channels the three-pass GEMM and output
+// transform stay ahead on small grids (128->256@14^2 B=16, 72 workgroups: 18.2
+// vs 20.0; 128->256@28^2 B=8, 104: 20.2 vs 21.2; 128->512@7^2 B=32: 21.4 vs
+// 24.1) and fall behind from 128 workgroups on (128->256@14^2 B=32 23.7 / 30.6
+// vs 21.0 / 27.9, B=48 29.1 vs 24.0; 128->256@28^2 B=12 24.2 vs 21.9, B=16
+// 26.7 vs 22.4; 96->256@14^2 B=32 23.1 vs 16.8; 64->256@28^2 B=16 25.0 vs
+// 16.8, B=20 28.2 vs 18.2; 128->192@14^2 B=48 26.1 vs 21.5): each two-pass
+// workgroup reads all Cp channels of its operands, so its time follows Cp,
+// not K.
 bool two_pass_wins(const Handle* Hd, const Shape& s) {
     if (!two_pass_possible(Hd->C, Hd->K)) return false;
     const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
     const int64_t v_bytes = 2 * gemm_out_v_elems(Hd->Cp, s.BP);
-    return grid >= 64 && grid <= Hd->cus && v_bytes <= (int64_t)20 << 20;
+    const int64_t min_grid = Hd->K > 128 ? 128 : 64;
+    return grid >= min_grid && grid <= Hd->cus && v_bytes <= (int64_t)20 << 20;
 }
 
 int choose_path(const Handle* Hd, const Shape& s) {
