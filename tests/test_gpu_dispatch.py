@@ -119,7 +119,7 @@ def test_auto_path_matches_three_pass(oracle, B, C, K, H, expect):
     assert oracle.rel_l2(a[:2].astype(np.float16), yo) <= 5e-3
 
 
-@pytest.mark.parametrize("path", [1, 3], ids=["3pass", "fused_block"])
+@pytest.mark.parametrize("path", [1, 3, 5, 6], ids=["3pass", "fused_block", "fused_small", "two_pass"])
 def test_graph_replay_matches_eager(path):
     """A forward captured in a HIP graph replays to the eager result, with
     eager work and synchronisation between replays."""
