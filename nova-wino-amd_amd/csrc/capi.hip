@@ -105,7 +105,7 @@ struct Handle {
     uint16_t* Uf = nullptr;  // U in MFMA fragment order (fused kernels)
     size_t Uf_cap = 0;       // bytes
     bool uf_ready = false;   // Uf holds the current weights' fragments
-    uint16_t* Uw = nullptr;  // U in the two-pass kernel's block order (path 6)
+    uint16_t* Uw = nullptr;  // U in 1 KB operand blocks (two-pass kernel, GEMV-like GEMMs)
     size_t Uw_cap = 0;       // bytes
     bool uw_ready = false;   // Uw holds the current weights' blocks
     void* ws = nullptr;
@@ -206,14 +206,15 @@ bool ensure_uf(Handle* H) {
     return H->uf_ready;
 }
 
-// The two-pass kernel's copy of U (launch_u_wfrag), built like Uf: at
-// set_weights when the automatic choice can pick path 6 or it is forced, else
-// on the first two-pass forward.
+// U in 1 KB operand blocks (launch_u_wfrag), read by the two-pass kernel and
+// by the three-pass GEMM at GEMV-like shapes (at most 32 tiles). Built like
+// Uf: at set_weights when the automatic choice can pick path 6 or it is
+// forced, else on the first forward that needs it.
 bool ensure_uw(Handle* H) {
     if (H->uw_ready) return true;
     const size_t need = (size_t)u_frag_elems(H->K, H->Cp) * sizeof(uint16_t);
     if ((int64_t)need >= ((int64_t)1 << 31)) {  // 32-bit offsets in the two-pass kernel
-        set_error(kErrInvalidArgument, "two-pass filter copy of %lld bytes exceeds 2^31 - 1",
+        set_error(kErrInvalidArgument, "filter block copy of %lld bytes exceeds 2^31 - 1",
                   (long long)need);
         return false;
     }
@@ -434,19 +435,27 @@ int choose_path(const Handle* Hd, const Shape& s) {
 }
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
+// blocks: the GEMM on operand blocks (GEMV-like shapes, wgemm_blocks), V in
+// the two-pass layout and U from the handle's block copy.
 bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* V,
-                    uint16_t* M, bool remember, const Epilogue& ep, bool timed = true) {
+                    uint16_t* M, bool remember, const Epilogue& ep, bool timed = true,
+                    bool blocks = false) {
     Profiler& pf = Hd->prof;
     const hipStream_t st = Hd->stream;
     const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
-    const uint16_t* U = Hd->U;
+    const uint16_t* U = blocks ? Hd->Uw : Hd->U;
     const bool nhwc = Hd->nhwc != 0;
-    const bool stream_v = wgemm_v_reads(K, (int)s.BP) <= 4;
+    const bool stream_v = !blocks && wgemm_v_reads(K, (int)s.BP) <= 4;
+    const int vfrag = blocks ? (Cp + 31) / 32 : 0;
+    const int64_t pstride = blocks ? gemm_out_v_elems(Cp, s.BP) / 64 : (int64_t)Cp * s.BP;
     auto in = [=]() {
-        return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp,
-                                      (int64_t)Cp * s.BP, st, nhwc, stream_v);
+        return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp, pstride, st,
+                                      nhwc, stream_v, vfrag);
     };
-    auto gm = [=]() { return launch_wgemm(U, V, M, K, Cp, (int)s.BP, st); };
+    auto gm = [=]() {
+        return blocks ? launch_wgemm_blocks(U, V, M, K, Cp, (int)s.BP, st)
+                      : launch_wgemm(U, V, M, K, Cp, (int)s.BP, st);
+    };
     auto out = [=]() {
         return launch_output_transform(M, y, s.B, K, s.Ho, s.Wo, s.nh, s.nw, K,
                                        (int64_t)K * s.BP, st, ep, nhwc);
@@ -465,7 +474,7 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
     if (!ok_in) return false;
     e = timed ? pf.arm() : SIZE_MAX;
     const bool ok_gm = hip_ok(gm(), "wgemm");
-    pf.done(kKindGemm, e, wgemm_name(K, Cp, (int)s.BP));
+    pf.done(kKindGemm, e, blocks ? wgemm_blocks_name((int)s.BP) : wgemm_name(K, Cp, (int)s.BP));
     if (!ok_gm) return false;
     e = timed ? pf.arm() : SIZE_MAX;
     const bool ok_out = hip_ok(out(), "output transform");
@@ -601,7 +610,14 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     // workspace for the largest sub-batch
     const int64_t Bc = std::min<int64_t>(chunk, s_all.B);
     const int64_t BPc = Bc * s_all.nh * s_all.nw;
-    const int64_t needV = path == 6 ? gemm_out_v_elems(Hd->Cp, BPc) : 64 * (int64_t)Hd->Cp * BPc;
+    // GEMV-like three-pass GEMMs (every sub-batch at most 32 tiles) read
+    // operand blocks: U's block copy is built here once per weights, which
+    // the allocation-free forward may not do
+    const bool blocks = (path == 1 || path == 4) && !no_alloc &&
+                        wgemm_blocks(Hd->K, Hd->Cp, (int)std::min<int64_t>(BPc, INT32_MAX));
+    if (blocks && !ensure_uw(Hd)) return;
+    const int64_t needV = (path == 6 || blocks) ? gemm_out_v_elems(Hd->Cp, BPc)
+                                                : 64 * (int64_t)Hd->Cp * BPc;
     const int64_t needM = 64 * (int64_t)Hd->K * BPc;
     uint16_t* V = nullptr;
     uint16_t* M = nullptr;
@@ -708,7 +724,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             if (!ok) return;
         } else if (path == 6) {
             if (!run_two_pass(Hd, xx, yy, s, V, b0 == 0, ep)) return;
-        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0 && !no_alloc, ep, !no_alloc)) {
+        } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0 && !no_alloc, ep, !no_alloc,
+                                   blocks)) {
             return;
         }
     }
@@ -1070,6 +1087,8 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s));
     const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;
     if (path == 6) return (long long)(gemm_out_v_elems(Hd->Cp, BPc) * 2);  // V only
+    if (wgemm_blocks(Hd->K, Hd->Cp, (int)std::min<int64_t>(BPc, INT32_MAX)))  // V in blocks + M
+        return (long long)((gemm_out_v_elems(Hd->Cp, BPc) + 64 * (int64_t)Hd->K * BPc) * 2);
     return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * BPc * 2);
 }
 

@@ -371,6 +371,139 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// GEMV-like shapes (BP <= 32) on 1 KB operand blocks: U from the two-pass
+// kernel's block copy (launch_u_wfrag: block (p, 16-row tile, 32-channel
+// step), lane l = row l % 16, channels 8*(l / 16) .. +7) and V in the
+// two-pass layout (launch_input_transform with vfrag = ceil(Cp / 32)), so
+// every operand fragment is one contiguous 1 KB load per wave; the product
+// layouts make it 16 rows x 64 bytes, two rows per 128-byte line with the
+// line's other half fetched by the next step. Wave = MT 16-row tiles of K x
+// all NT 16-tile blocks of BP; PD steps in flight; M leaves in the product
+// layout [64][BP][K] for the output transform. Same lane layout and
+// channel-step order as the other GEMM kernels: M is bit-identical. Measured
+// on MI355X (back-to-back launches, us, product-layout kernel -> blocks):
+// 512@7^2 batch 1 6.5 -> 4.6, batch 4 8.8 -> 4.7, batch 8 (32 tiles) 7.8 ->
+// 6.5; 256@14^2 batch 1 3.1 -> 2.8, batch 3 4.1 -> 3.3; 128@28^2 batch 1 (25
+// tiles) 3.1 -> 2.7; 1280@8^2 batch 1 33.4 -> 30.4, batch 2 35.1 -> 30.6 (U
+// at 6.9 TB/s); 1280@16^2 batch 2 (18 tiles) 33.7 -> 31.3. Past 32 tiles
+// (three blocks per wave) it won at 3 of 4 shapes and lost 7 % at 640@32^2
+// batch 1, so the LDS-tiled kernels keep those.
+// ---------------------------------------------------------------------------
+template <int MT, int NT, int PD, int WPB>
+__global__ __launch_bounds__(64 * WPB) void wgemm_block_kernel(
+    const _Float16* __restrict__ Uw, const _Float16* __restrict__ Vb, _Float16* __restrict__ M,
+    int K, int Cp, int BP, int u_bytes, int v_bytes, int m_bytes) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int nkt = (K + 15) / 16;
+    const int nkg = (nkt + MT - 1) / MT;
+    // XCD-aware: each XCD takes a contiguous run of positions
+    const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x) * WPB + wave;
+    if (item >= 64 * nkg) return;  // no barrier below: idle waves may leave
+    const int p = item / nkg;
+    const int kt0 = (item - p * nkg) * MT;
+    const int nsteps = (Cp + 31) / 32;
+    const int nbb = (BP + 15) / 16;  // <= NT
+    const int r16 = lane & 15, g = lane >> 4;
+    const __amdgpu_buffer_rsrc_t urs = make_rsrc(Uw, u_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(Vb, v_bytes);
+    const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, m_bytes);
+    // U blocks hold zeros past K and Cp; V slots of tiles past BP and of
+    // channels past Cp are never written, so those lanes read through
+    // out-of-range offsets
+    int aoff[MT], boff[NT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+        aoff[i] = kt0 + i < nkt ? (p * nkt + kt0 + i) * nsteps * 1024 + lane * 16 : kOob;
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+        boff[n] = 16 * n + r16 < BP ? ((p * nbb + n) * nsteps) * 1024 + lane * 16 : kOob;
+    h8 a[PD][MT], b[PD][NT];
+    auto load = [&](int j, h8 (&af)[MT], h8 (&bf)[NT]) {
+        const bool cok = j < nsteps && 32 * j + 8 * g < Cp;  // Cp % 8 == 0: whole groups
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+            af[i] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               urs, j < nsteps ? aoff[i] : kOob, j * 1024, 0));
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+            bf[n] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                               vrs, cok ? boff[n] : kOob, j * 1024, 0));
+    };
+    f4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int n = 0; n < NT; n++) acc[i][n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < PD; j++) load(j, a[j], b[j]);
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; j++) {
+            if (s0 + j >= nsteps) break;
+#pragma unroll
+            for (int i = 0; i < MT; i++)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+                    acc[i][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][i], b[j][n],
+                                                                       acc[i][n], 0, 0, 0);
+            if (s0 + PD + j < nsteps) load(s0 + PD + j, a[j], b[j]);
+        }
+    }
+    const int mu = 2 * p * BP * K;  // uniform
+    const bool vec_store = (K & 3) == 0;
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int k = (kt0 + i) * 16 + 4 * g;
+            const int bp = 16 * n + r16;
+            const int off = bp < BP ? 2 * (bp * K + k) : kOob;
+            if (vec_store) {
+                h4 v = {(_Float16)acc[i][n][0], (_Float16)acc[i][n][1], (_Float16)acc[i][n][2],
+                        (_Float16)acc[i][n][3]};
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, v), mrs,
+                                                      k < K ? off : kOob, mu, 0);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        __builtin_bit_cast(uint16_t, (_Float16)acc[i][n][e]), mrs,
+                        k + e < K ? off + 2 * e : kOob, mu, 0);
+            }
+        }
+}
+
+bool wgemm_blocks(int K, int Cp, int BP) {
+    return BP <= 32 && 2 * u_frag_elems(K, Cp) < ((int64_t)1 << 31) &&
+           2 * (int64_t)64 * BP * K < ((int64_t)1 << 31);
+}
+
+hipError_t launch_wgemm_blocks(const uint16_t* Uw, const uint16_t* Vb, uint16_t* M, int K,
+                               int Cp, int BP, hipStream_t s) {
+    if (!wgemm_blocks(K, Cp, BP) || Cp % 8 != 0) return hipErrorInvalidValue;
+    if (BP == 0) return hipSuccess;
+    constexpr int kMT = 2, kPD = 4, kWPB = 2;
+    const int nkg = ((K + 15) / 16 + kMT - 1) / kMT;
+    const unsigned grid = (unsigned)((64 * nkg + kWPB - 1) / kWPB);
+    auto go = [&](auto kernel) {
+        launch(kernel, dim3(grid), dim3(64 * kWPB), s, reinterpret_cast<const _Float16*>(Uw),
+               reinterpret_cast<const _Float16*>(Vb), reinterpret_cast<_Float16*>(M), K, Cp, BP,
+               (int)(2 * u_frag_elems(K, Cp)), (int)(2 * gemm_out_v_elems(Cp, BP)),
+               (int)(2 * (int64_t)64 * BP * K));
+    };
+    if (BP <= 16)
+        go(wgemm_block_kernel<kMT, 1, kPD, kWPB>);
+    else
+        go(wgemm_block_kernel<kMT, 2, kPD, kWPB>);
+    return hipGetLastError();
+}
+
+const char* wgemm_blocks_name(int BP) {
+    return BP <= 16 ? "wgemm_block_kernel<2, 1, 4, 2>" : "wgemm_block_kernel<2, 2, 4, 2>";
+}
+
 // Kernel per shape. Register-direct 64 x 16 for GEMV-like batch-1 deep
 // layers (BP <= 16: few tiles; two 16-row tiles per wave, which halves the V
 // fragment loads and doubles the U bytes each wave keeps in flight: 512@7^2

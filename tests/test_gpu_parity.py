@@ -122,8 +122,10 @@ def test_output_transform_bitexact(oracle, B, K, Ho, Wo):
     assert_same_bits(_u16(y), ref, "y")
 
 
-# GEMM shapes by tile kernel (wgemm_cfg): BP <= 16 and small grids first
-# (register-direct and 64 x 64 kernels), larger BP with K, Cp <= 128 (several
+# GEMM shapes by tile kernel: at most 32 tiles first (the operand-block
+# kernel: its V is in blocks, so only M is read back; the product-layout
+# register-direct kernel it replaces is compared with it bit for bit in
+# test_gpu_gemv_blocks.py), small grids (64 x 64), larger BP with K, Cp <= 128 (several
 # bp tiles per position, two stages in flight), partial 32-channel steps, K not
 # a multiple of 4; K >= 512 from 128 tiles (64 x 128, with a partial k tile
 # and a partial bp tile), K > 256 below 128 tiles (the four-wave 64 x 64
@@ -143,8 +145,9 @@ GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256,
 @pytest.mark.parametrize("B,C,K,H", GEMM_CASES)
 def test_gemm_within_fp32_bound(oracle, B, C, K, H):
     """White-box: force the 3-pass path with caller workspaces; for C % 8 == 0
-    the workspace then holds V[64][BP][C] and M[64][BP][K] at the minimal
-    tiling ceil(Ho/6) x ceil(Wo/6)."""
+    the workspace then holds V[64][BP][C] (above 32 tiles; at most 32 the GEMM
+    reads V in operand blocks, checked through M) and M[64][BP][K] at the
+    minimal tiling ceil(Ho/6) x ceil(Wo/6)."""
     print(f"[gemm] B={B} C={C} K={K} H={H}", flush=True)
     assert C % 8 == 0
     lib = _lib()
@@ -172,7 +175,8 @@ def test_gemm_within_fp32_bound(oracle, B, C, K, H):
     Vg = V[: 64 * C * BPm].view(64, BPm, C)
     Mg = M[: 64 * K * BPm].view(64, BPm, K)
     Vo = oracle.input_transform(x.numpy(), 1, nhm, nwm)
-    assert_same_bits(_u16(Vg), Vo, "V (workspace)")
+    if BPm > 32:
+        assert_same_bits(_u16(Vg), Vo, "V (workspace)")
     Uo = oracle.filter_transform(w.numpy())
     Mo, Mabs = oracle.batched_gemm(Uo, Vo, with_abs=True)
     mg = Mg.float().cpu().numpy().astype(np.float64)

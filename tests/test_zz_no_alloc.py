@@ -58,7 +58,7 @@ def _pair(lib, h, x, K, pad=1, nhwc=False):
 # (C, K, H, pad, first batch, second batch, expected path): second call smaller
 CASES = [
     (128, 128, 28, 1, 8, 3, 1),     # three-pass, conv3_x
-    (64, 64, 56, 1, 32, 16, 3),     # fused tile-block, conv2_x (no workspace)
+    (64, 64, 56, 1, 32, 24, 3),     # fused tile-block, conv2_x (no workspace)
     (512, 512, 7, 1, 32, 1, 1),     # three-pass, conv5_x, then batch 1
     (100, 24, 17, 0, 6, 2, 1),      # C % 8 != 0 (padded channel pitch), pad 0
     (40, 24, 17, 0, 6, 2, 5),       # the small-problem fused kernel (no workspace)
