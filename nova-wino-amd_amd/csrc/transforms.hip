@@ -279,8 +279,11 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     const int t = threadIdx.x / G::kCB;
     const int tw = tw0 + t;
     const int c = c0 + cc;
+    // slots past the last tile or channel have nothing to store (no barrier
+    // follows: whole idle waves retire and free their SIMD)
+    if (tw >= nw || c >= ldv) return;
     const int bp = (b * nh + th) * nw + tw;
-    const int voff = (tw < nw && c < ldv) ? v_plane_off(bp, c, ldv, vfrag) : kOob;
+    const int voff = v_plane_off(bp, c, ldv, vfrag);
     unsigned cmask = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -388,8 +391,9 @@ __global__ __launch_bounds__(256) void input_nhwc_kernel(
     const int t = threadIdx.x / kCB;
     const int tw = tw0 + t;
     const int c = c0 + cc;
+    if (tw >= nw || c >= ldv) return;  // nothing to store; no barrier follows
     const int bp = (b * nh + th) * nw + tw;
-    const int voff = (tw < nw && c < ldv) ? v_plane_off(bp, c, ldv, vfrag) : kOob;
+    const int voff = v_plane_off(bp, c, ldv, vfrag);
     const _Float16* src = sx + 6 * t * kPix + cc;
     input_tile_rows([&](int i, int j) { return (float)src[(i * kCols + j) * kPix]; },
                     [&](int r, int s2, float v) {
@@ -618,13 +622,16 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     const __amdgpu_buffer_rsrc_t mrs = make_rsrc(M, m_bytes);
     const __amdgpu_buffer_rsrc_t yrs = make_rsrc(y, y_bytes);
 
-    {
+    // slots past the last tile or channel skip the transform (the store
+    // phase never reads their LDS rows); whole idle waves wait at the barrier
+    // without issuing
+    if (tw0 + (int)threadIdx.x / G::kKB < nw && k0 + (int)threadIdx.x % G::kKB < K) {
         const int kk = threadIdx.x % G::kKB;
         const int t = threadIdx.x / G::kKB;
         const int tw = tw0 + t;
         const int k = k0 + kk;
         const int bp = (b * nh + th) * nw + tw;
-        const int moff = (tw < nw && k < K) ? 2 * (bp * ldm + k) : kOob;
+        const int moff = 2 * (bp * ldm + k);
         uint16_t m[64];
 #pragma unroll
         for (int p = 0; p < 64; p++)
@@ -633,7 +640,7 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
         output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
                     out);
         _Float16* sp = sy + kk * G::kPlane + t * 6;
-        const ChannelEpilogue<kEpi> epi(bias, k < K ? k : 0, res ? 0 : relu);
+        const ChannelEpilogue<kEpi> epi(bias, k, res ? 0 : relu);
 #pragma unroll
         for (int r = 0; r < 6; r++)
 #pragma unroll
