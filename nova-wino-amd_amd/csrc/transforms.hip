@@ -528,14 +528,15 @@ static int pick_tw(int64_t rows, int n, int ch) {
 // kernels, which issue half as many memory instructions per patch (measured
 // on MI355X: lane-parallel input 5.5 us vs 6.8 us for ResNet-50 conv2_x at
 // batch 1, 20.2 us vs 14.0 us at batch 32).
-static bool latency_bound(int64_t rows, int n, int ch) {
+static int64_t widest_grid(int64_t rows, int n, int ch) {
     int64_t widest_g = 0;
     for (int tw = 8; tw >= 2; tw /= 2) {
         const int cb = 256 / tw;
         widest_g = std::max(widest_g, (int64_t)((n + tw - 1) / tw) * ((ch + cb - 1) / cb) * rows);
     }
-    return widest_g < 256;
+    return widest_g;
 }
+static bool latency_bound(int64_t rows, int n, int ch) { return widest_grid(rows, n, ch) < 256; }
 
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
@@ -950,7 +951,14 @@ static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K,
 hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K, int Ho,
                                    int Wo, int nh, int nw, int ldm, int64_t pstride,
                                    hipStream_t s, Epilogue ep, bool nhwc) {
-    if (latency_bound((int64_t)B * nh, nw, K))
+    // An odd output row pitch leaves the NCHW tile-block kernel one 2-byte
+    // store per output; on images one or two tiles wide the lane-parallel
+    // form then wins up to 640 workgroups (us, tile-block vs lane-parallel:
+    // 512@7^2 batch 16 (512 workgroups) 7.0 vs 5.5, 256@7^2 batch 32 (512)
+    // 7.1 vs 5.5, 512@7^2 batch 24 (768) 7.0 vs 6.9, batch 32 (1024) 7.0 vs
+    // 8.7; five tiles wide, 130@27^2 batch 12 (300), it lost: 7.7 vs 8.2).
+    const int64_t widest = widest_grid((int64_t)B * nh, nw, K);
+    if (widest < 256 || (!nhwc && (Wo & 1) != 0 && nw <= 2 && widest < 640))
         return launch_output_lp(M, y, B, K, Ho, Wo, nh, nw, ldm, pstride, s, ep, nhwc);
     if (nhwc) {
         const int tw = pick_tw((int64_t)B * nh, nw, K);

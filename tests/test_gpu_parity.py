@@ -104,8 +104,12 @@ def test_input_transform_bitexact(oracle, B, C, H, W, pad):
     assert_same_bits(_u16(V), ref, "V")
 
 
+# Output: the lane-parallel kernel below 256 tile-block workgroups, and for
+# an odd row pitch on images at most two tiles wide below 640 ((16, 512, 7,
+# 7)); the tile-block kernel for (8, 64, 56, 56) and, odd rows, (12, 130, 27,
+# 29) and (32, 130, 27, 29).
 OUTPUT_CASES = [(1, 64, 56, 56), (2, 48, 14, 14), (1, 130, 7, 9), (3, 8, 13, 11), (1, 16, 1, 1),
-                (8, 64, 56, 56), (12, 130, 27, 29)]
+                (8, 64, 56, 56), (12, 130, 27, 29), (16, 512, 7, 7), (32, 130, 27, 29)]
 
 
 @pytest.mark.parametrize("B,K,Ho,Wo", OUTPUT_CASES)
