@@ -212,6 +212,46 @@ struct InGeom {
     __device__ static int base(int c) { return c * kCP; }
 };
 
+// Staging of the tile-block input transforms: the strip's 8 input rows of
+// every channel of the block, copied into LDS as whole 16-byte-aligned row
+// spans. Thread = row r (tid % 8) of channels tid / 8 + 32u; each thread
+// copies whole row spans (kNJ 16-byte loads at immediate offsets); its spans
+// are 32 channels apart, a constant byte step, and their LDS destinations are
+// immediate offsets. The whole offset stays in the range-checked vector
+// offset, so span bytes past the end of x read zero, as do rows outside the
+// image and channels past C.
+template <int TW>
+__device__ __forceinline__ void input_stage(unsigned char* sx, __amdgpu_buffer_rsrc_t xrs,
+                                            int xbase, int C, int H, int W, int HW, int h0,
+                                            int c0) {
+    using G = InGeom<TW>;
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    const int r = threadIdx.x & 7, c = threadIdx.x >> 3;
+    const int h = h0 + r;
+    const bool row_ok = h >= 0 && h < H;
+    // 64*HW bytes per 32 channels is a multiple of 16: every span of this
+    // thread starts at the same offset within its 16-byte granule
+    const int ga = (xbase + 2 * (c * HW + h * W)) & ~15;
+    unsigned char* dst = sx + G::base(c) + r * G::kRP;
+    u4 val[G::kUnits][G::kNJ];
+#pragma unroll
+    for (int u = 0; u < G::kUnits; u++) {
+        const int vo = (row_ok && c0 + c + 32 * u < C) ? ga + 64 * u * HW : kOob;
+#pragma unroll
+        for (int q = 0; q < G::kNJ; q++)
+            val[u][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, vo + 16 * q, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < G::kUnits; u++)
+#pragma unroll
+        for (int q = 0; q < G::kNJ; q++) {
+            unsigned char* d = dst + 32 * u * G::kCP + 16 * q;
+            *reinterpret_cast<u2*>(d) = u2{val[u][q][0], val[u][q][1]};
+            *reinterpret_cast<u2*>(d + 8) = u2{val[u][q][2], val[u][q][3]};
+        }
+}
+
 template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
@@ -237,41 +277,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x_al, x_bytes);
     const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
 
-    // ---- staging: thread = row r (tid % 8) of channels tid / 8 + 32u ----
-    // Each thread copies whole row spans (kNJ 16-byte loads at immediate
-    // offsets); its spans are 32 channels apart, a constant byte step, and
-    // their LDS destinations are immediate offsets. The whole offset stays in
-    // the range-checked vector offset, so span bytes past the end of x read
-    // zero.
-    {
-        typedef unsigned u4 __attribute__((ext_vector_type(4)));
-        typedef unsigned u2 __attribute__((ext_vector_type(2)));
-        const int r = threadIdx.x & 7, c = threadIdx.x >> 3;
-        const int h = h0 + r;
-        const bool row_ok = h >= 0 && h < H;
-        // 64*HW bytes per 32 channels is a multiple of 16: every span of this
-        // thread starts at the same offset within its 16-byte granule
-        const int ga = (xbase + 2 * (c * HW + h * W)) & ~15;
-        unsigned char* dst = sx + G::base(c) + r * G::kRP;
-        u4 val[G::kUnits][G::kNJ];
-#pragma unroll
-        for (int u = 0; u < G::kUnits; u++) {
-            // rows outside the image and channels past C: out-of-range offset,
-            // the loads return zeros
-            const int vo = (row_ok && c0 + c + 32 * u < C) ? ga + 64 * u * HW : kOob;
-#pragma unroll
-            for (int q = 0; q < G::kNJ; q++)
-                val[u][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, vo + 16 * q, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < G::kUnits; u++)
-#pragma unroll
-            for (int q = 0; q < G::kNJ; q++) {
-                unsigned char* d = dst + 32 * u * G::kCP + 16 * q;
-                *reinterpret_cast<u2*>(d) = u2{val[u][q][0], val[u][q][1]};
-                *reinterpret_cast<u2*>(d + 8) = u2{val[u][q][2], val[u][q][3]};
-            }
-    }
+    input_stage<TW>(sx, xrs, xbase, C, H, W, HW, h0, c0);
     __syncthreads();
 
     // ---- compute: (tile t, channel cc) per thread, lanes over channels ----
