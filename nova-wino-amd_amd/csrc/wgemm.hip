@@ -521,18 +521,32 @@ const char* wgemm_blocks_name(int BP) {
 //    256@14^2 B=32 9.5 vs 11.0, B=128 24.6 vs 29.1; 512@7^2 B=32 10.8 vs
 //    11.2 for 128 x 128; 128@28^2 B=128 23.0 vs 26.0; SD-1.5 640@32^2 B=2
 //    14.4 vs 15.6, 320@64^2 B=2 8.8 vs 9.7; SDXL 640@64^2 14.5 vs 17.7;
-//    1280->640@32^2 B=2 23.6 vs 30.4);
+//    1280->640@32^2 B=2 23.6 vs 30.4). A second sweep (back-to-back launches
+//    of the GEMM alone) favoured it for K <= 128 from 200 tiles as well
+//    (128@28^2 B=32 7.17 -> 6.38), but inside forwards, with V just written,
+//    it lost there (batch 32 8.95 -> 9.41 us per GEMM), so 64 x 64 stays;
+//  * 64 x 96 with four waves and one stage in flight where that tile width
+//    fills its last tile 15 points better than 128 (GEMM alone, us:
+//    256@14^2 B=32, 288 tiles, 6.98 -> 6.39; 640@32^2 B=2, 72 tiles, 13.9 ->
+//    12.4, with 320 -> 640 channels 7.9 -> 7.3, 1280 -> 640 24.0 -> 21.2;
+//    640@32^2 B=4 21.3 -> 19.9; inside forwards 640@32^2 B=2 13.2 -> 11.9,
+//    whole forward 30.0 -> 28.5; 256@14^2 B=32 unchanged, 9.1 vs 9.0); where
+//    the fills are close 64 x 128 stays ahead (256@14^2 B=64 12.5 vs 12.4,
+//    128@28^2 B=64 11.9 vs 12.4);
 //  * else 64 x 64: two stages in flight from 128 tiles (128@28^2 B=32 8.7,
 //    128 x 128 8.7, 64 x 128 8.9; 256@14^2 B=16 7.5 vs 8.1 for 64 x 128),
 //    8 waves up to K = 256, 4 waves beyond (512@7^2 B=8 7.7 vs 8.0 with 8
 //    waves and 9.0 with 64 x 128; B=16 8.0 vs 9.3).
+// Share of a row of bp tiles of width tb that holds real tiles.
+static double bp_fill(int BP, int tb) { return (double)BP / (tb * ((BP + tb - 1) / tb)); }
+
 static int wgemm_cfg(int K, int BP) {
     if (BP <= 16) return 0;
     if (K >= 512 && BP >= 256) return 2;
     if (K >= 1024 && BP < 128) return 5;
     if ((K >= 640 && BP >= 64) || (K >= 512 && BP >= 128) || (K >= 256 && BP >= 200) ||
         (K <= 128 && BP >= 1600))
-        return 6;
+        return bp_fill(BP, 96) >= bp_fill(BP, 128) + 0.15 ? 7 : 6;
     if (BP >= 128) return 3;
     return K <= 256 ? 4 : 1;
 }
@@ -550,7 +564,8 @@ const char* wgemm_name(int K, int Cp, int BP) {
                                   "wgemm_lds_kernel<64, 64, 2, 4, 2>",
                                   "wgemm_lds_kernel<64, 64, 2, 4, 1>",
                                   "wgemm_lds_kernel<128, 64, 2, 4, 1>",
-                                  "wgemm_lds_kernel<64, 128, 2, 4, 2>"};
+                                  "wgemm_lds_kernel<64, 128, 2, 4, 2>",
+                                  "wgemm_lds_kernel<64, 96, 2, 2, 1>"};
     return names[wgemm_cfg(K, BP)];
 }
 
@@ -563,6 +578,7 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
         case 3: return launch_lds<64, 64, 2, 4, 2>(U, V, M, K, Cp, BP, s);
         case 5: return launch_lds<128, 64, 2, 4, 1>(U, V, M, K, Cp, BP, s);
         case 6: return launch_lds<64, 128, 2, 4, 2>(U, V, M, K, Cp, BP, s);
+        case 7: return launch_lds<64, 96, 2, 2, 1>(U, V, M, K, Cp, BP, s);
         default: return launch_lds<64, 64, 2, 4, 1>(U, V, M, K, Cp, BP, s);
     }
 }

@@ -135,7 +135,9 @@ def test_output_transform_bitexact(oracle, B, K, Ho, Wo):
 # and a partial bp tile), K > 256 below 128 tiles (the four-wave 64 x 64
 # kernel); then 64 x 128 at K <= 128 from 1600 tiles (16 x 64@56^2), K >= 256
 # from 200 and K >= 640 from 64, 128 x 128 at K >= 512 from 256 tiles, and
-# 128 x 64 at K >= 1024 below 128 tiles, each with partial tiles.
+# 128 x 64 at K >= 1024 below 128 tiles, each with partial tiles; last the
+# 64 x 96 tile (288 tiles at K = 256, 72 at K = 640) and 64 x 64 at K <= 128
+# below 1600 tiles (225 tiles, K = 120).
 GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256, 28),
               (1, 256, 256, 14), (1, 16, 40, 9), (8, 128, 128, 28), (2, 136, 200, 30),
               (4, 72, 132, 40),
@@ -143,7 +145,8 @@ GEMM_CASES = [(1, 64, 64, 56), (1, 512, 512, 7), (2, 192, 48, 14), (4, 128, 256,
               (12, 96, 98, 28),
               (32, 40, 520, 7), (33, 24, 516, 7),
               (2, 64, 320, 14), (3, 48, 264, 20),
-              (8, 40, 264, 28), (2, 32, 648, 32), (66, 24, 516, 7), (1, 16, 1032, 28)]
+              (8, 40, 264, 28), (2, 32, 648, 32), (66, 24, 516, 7), (1, 16, 1032, 28),
+              (32, 64, 256, 14), (2, 40, 640, 32), (9, 56, 120, 28)]
 
 
 @pytest.mark.parametrize("B,C,K,H", GEMM_CASES)
