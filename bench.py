@@ -13,7 +13,8 @@ Reported on one JSON line (stdout):
                (2*B*K*C*Ho*Wo*9, /root/reference/benchmarks/bench_layers.py:58)
                / step time
   layers       per layer: NOVA ms and MIOpen (nn.Conv2d fp16) ms, eager and
-               HIP-graph replayed, effective TFLOP/s, path, roofline fraction
+               HIP-graph replayed (ten forwards per graph: GPU time),
+               effective TFLOP/s, path, roofline fraction
                T_roof/T (T_roof = max(2*64*K*C*B*P_min / 2.5 PF,
                (2BCHW + 2BKHoWo + 2*64*K*C) / 8 TB/s)), warm and cold
   roofline     the dominant kernel family of the step (largest summed time),
@@ -51,6 +52,7 @@ BATCHES = [1, 32]
 PEAK_HBM_GBS = 8000.0
 PEAK_FP16_TFLOPS = 2500.0
 KIND_NAMES = ["input", "gemm", "output", "fused"]
+GRAPH_CALLS = 10  # forwards captured per layer graph (per-layer GPU time)
 PATH_NAMES = {1: "3-pass", 2: "fused_rows", 3: "fused_block", 4: "windowed", 5: "fused_small",
               6: "two_pass"}
 
@@ -108,9 +110,9 @@ def time_region(fn, reps, torch):
     return s.elapsed_time(e) / reps
 
 
-def graph_of(fn, torch):
-    """Capture fn into a HIP graph (after an eager warm-up); None if capture
-    is not possible."""
+def graph_of(fn, torch, n=1):
+    """Capture n calls of fn into one HIP graph (after an eager warm-up);
+    None if capture is not possible."""
     try:
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -120,7 +122,8 @@ def graph_of(fn, torch):
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            fn()
+            for _ in range(n):
+                fn()
         torch.cuda.synchronize()
         return g
     except Exception as exc:  # report, do not hide: the field becomes null
@@ -901,12 +904,15 @@ def main():
             if not args.no_miopen:
                 r["miopen_ms"] = time_region(lambda: mio(x), args.layer_reps, torch)
             if not args.no_graph:
-                g = graph_of(lambda: mod(x), torch)
-                r["nova_graph_ms"] = (time_region(g.replay, args.layer_reps, torch)
+                # ten forwards per graph: one replay's host cost (~16-20 us)
+                # is spread over ten layers' GPU time, so this reads the GPU
+                g = graph_of(lambda: mod(x), torch, GRAPH_CALLS)
+                reps = max(10, args.layer_reps // GRAPH_CALLS)
+                r["nova_graph_ms"] = (time_region(g.replay, reps, torch) / GRAPH_CALLS
                                       if g is not None else None)
                 if not args.no_miopen:
-                    gm = graph_of(lambda: mio(x), torch)
-                    r["miopen_graph_ms"] = (time_region(gm.replay, args.layer_reps, torch)
+                    gm = graph_of(lambda: mio(x), torch, GRAPH_CALLS)
+                    r["miopen_graph_ms"] = (time_region(gm.replay, reps, torch) / GRAPH_CALLS
                                             if gm is not None else None)
 
     # ---- dominant kernel roofline -----------------------------------------------
