@@ -120,7 +120,8 @@ hipError_t launch_wgemm(const uint16_t* U, const uint16_t* V, uint16_t* M, int K
 int wgemm_v_reads(int K, int BP);
 // Kernel name (template configuration) launch_wgemm picks for this shape.
 const char* wgemm_name(int K, int Cp, int BP);
-// GEMV-like shapes (BP <= 32, U block copy under 2^31 bytes): the GEMM on
+// GEMV-like shapes (BP <= 32, or 48 above K = 1024; U block copy under
+// 2^31 bytes): the GEMM on
 // operand blocks, Uw from launch_u_wfrag and V in the two-pass layout
 // (launch_input_transform with vfrag = ceil(Cp / 32)); M as launch_wgemm's,
 // bit-identical.

@@ -372,7 +372,7 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 }
 
 // ---------------------------------------------------------------------------
-// GEMV-like shapes (BP <= 32) on 1 KB operand blocks: U from the two-pass
+// GEMV-like shapes (BP <= 32, or 48 above K = 1024) on 1 KB operand blocks: U from the two-pass
 // kernel's block copy (launch_u_wfrag: block (p, 16-row tile, 32-channel
 // step), lane l = row l % 16, channels 8*(l / 16) .. +7) and V in the
 // two-pass layout (launch_input_transform with vfrag = ceil(Cp / 32)), so
@@ -387,8 +387,11 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 // 6.5; 256@14^2 batch 1 3.1 -> 2.8, batch 3 4.1 -> 3.3; 128@28^2 batch 1 (25
 // tiles) 3.1 -> 2.7; 1280@8^2 batch 1 33.4 -> 30.4, batch 2 35.1 -> 30.6 (U
 // at 6.9 TB/s); 1280@16^2 batch 2 (18 tiles) 33.7 -> 31.3. Past 32 tiles
-// (three blocks per wave) it won at 3 of 4 shapes and lost 7 % at 640@32^2
-// batch 1, so the LDS-tiled kernels keep those.
+// (three blocks per wave) it won at 3 of 4 shapes (1280@32^2 batch 1, 36
+// tiles, 35.2 -> 33.3; 512@7^2 batch 12 8.1 -> 7.3) and lost 7 % at 640@32^2
+// batch 1, so it takes 33-48 tiles only above K = 1024 (whole forwards in a
+// graph, us: 1280@32^2 batch 1 51.0 -> 49.0, 1280@36^2 51.7 -> 49.8; 1024@32^2
+// batch 1 36.3 -> 36.5).
 // ---------------------------------------------------------------------------
 template <int MT, int NT, int PD, int WPB>
 __global__ __launch_bounds__(64 * WPB) void wgemm_block_kernel(
@@ -476,7 +479,7 @@ __global__ __launch_bounds__(64 * WPB) void wgemm_block_kernel(
 }
 
 bool wgemm_blocks(int K, int Cp, int BP) {
-    return BP <= 32 && 2 * u_frag_elems(K, Cp) < ((int64_t)1 << 31) &&
+    return (BP <= 32 || (BP <= 48 && K > 1024)) && 2 * u_frag_elems(K, Cp) < ((int64_t)1 << 31) &&
            2 * (int64_t)64 * BP * K < ((int64_t)1 << 31);
 }
 
@@ -495,13 +498,17 @@ hipError_t launch_wgemm_blocks(const uint16_t* Uw, const uint16_t* Vb, uint16_t*
     };
     if (BP <= 16)
         go(wgemm_block_kernel<kMT, 1, kPD, kWPB>);
-    else
+    else if (BP <= 32)
         go(wgemm_block_kernel<kMT, 2, kPD, kWPB>);
+    else
+        go(wgemm_block_kernel<kMT, 3, kPD, kWPB>);
     return hipGetLastError();
 }
 
 const char* wgemm_blocks_name(int BP) {
-    return BP <= 16 ? "wgemm_block_kernel<2, 1, 4, 2>" : "wgemm_block_kernel<2, 2, 4, 2>";
+    return BP <= 16   ? "wgemm_block_kernel<2, 1, 4, 2>"
+           : BP <= 32 ? "wgemm_block_kernel<2, 2, 4, 2>"
+                      : "wgemm_block_kernel<2, 3, 4, 2>";
 }
 
 // Kernel per shape. Register-direct 64 x 16 for GEMV-like batch-1 deep

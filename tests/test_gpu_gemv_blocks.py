@@ -25,7 +25,7 @@ def _lib():
     return get_lib()
 
 
-# (B, C, K, H, pad): tiles = B * ceil(Ho / 6)^2 <= 32
+# (B, C, K, H, pad): tiles = B * ceil(Ho / 6)^2 <= 32, or <= 48 above K = 1024
 CASES = [
     (1, 512, 512, 7, 1),    # ResNet-50 conv5_x, 4 tiles
     (1, 256, 256, 14, 1),   # conv4_x, 9 tiles
@@ -37,6 +37,7 @@ CASES = [
     (1, 128, 128, 28, 1),   # conv3_x: 25 tiles, a partial second block
     (8, 512, 512, 7, 1),    # exactly 32 tiles
     (3, 72, 36, 14, 1),     # 27 tiles, K % 16 != 0, Cp = 72
+    (1, 64, 1040, 32, 1),   # 36 tiles above K = 1024: three tile blocks per wave
 ]
 
 
