@@ -445,7 +445,14 @@ bool run_three_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, 
     const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
     const uint16_t* U = blocks ? Hd->Uw : Hd->U;
     const bool nhwc = Hd->nhwc != 0;
-    const bool stream_v = !blocks && wgemm_v_reads(K, (int)s.BP) <= 4;
+    // V streamed past the L2 (nt stores) when the GEMM reads it at most 4
+    // times and it holds at most 24 MB; larger V are read faster from the L2
+    // (whole forwards in a graph, us, streamed vs not: ResNet-50 batch 128
+    // 128@28^2 (V 52 MB) 61.3 vs 58.1, 256@14^2 (38 MB) 52.1 vs 50.6, 512@7^2
+    // (34 MB) 54.7 vs 50.9; batch 64 128@28^2 (26 MB) 37.5 vs 37.2; batch 32
+    // 128@28^2 (13 MB) 27.1 vs 28.8, 256@14^2 (9 MB) 26.1 vs 27.1)
+    const bool stream_v = !blocks && wgemm_v_reads(K, (int)s.BP) <= 4 &&
+                          2 * (int64_t)64 * Cp * s.BP <= ((int64_t)24 << 20);
     const int vfrag = blocks ? (Cp + 31) / 32 : 0;
     const int64_t pstride = blocks ? gemm_out_v_elems(Cp, s.BP) / 64 : (int64_t)Cp * s.BP;
     auto in = [=]() {
