@@ -444,7 +444,10 @@ def kernel_stats_from(trace_dir, bench_json, out_path):
               "The bench line's per-family times are hipEvents recorded by each kernel's own "
               "dispatch packet over a timed region of the unprofiled run (first command); the "
               "trace's are End - Start of every launch of the family in the profiled run "
-              "(call-weighted over the step's layers, as the bench averages them).", "",
+              "(call-weighted over the step's layers, as the bench averages them). The event "
+              "pair also holds each dispatch's wait behind the kernel before it (the barrier "
+              "and cache flush between dependent launches), which the trace leaves out: about "
+              "0.1-1.3 us per launch, so the ratio runs from 1.0 to 1.3 with the box.", "",
               "| family | bench avg_launch_us | rocprofv3 mean us | calls | ratio |",
               "|---|---:|---:|---:|---:|"]
     fams = line.get("kernel_families", {})
