@@ -511,11 +511,14 @@ const char* wgemm_blocks_name(int BP) {
                       : "wgemm_block_kernel<2, 3, 4, 2>";
 }
 
-// Kernel per shape. Register-direct 64 x 16 for GEMV-like batch-1 deep
-// layers (BP <= 16: few tiles; two 16-row tiles per wave, which halves the V
-// fragment loads and doubles the U bytes each wave keeps in flight: 512@7^2
-// at batch 1 7.1 -> 6.5 us, 1280@8^2 at batch 2 39.2 -> 34.9 us); LDS-tiled
-// otherwise, the tile chosen from a sweep of every tile shape on MI355X
+// Kernel per shape on the product layouts (the operand-block kernel above
+// takes GEMV-like shapes when the handle can hold U's block copy; this rule
+// serves the rest, and the allocation-free forward). Register-direct 64 x 16
+// for GEMV-like batch-1 deep layers (BP <= 16: few tiles; two 16-row tiles
+// per wave, which halves the V fragment loads and doubles the U bytes each
+// wave keeps in flight: 512@7^2 at batch 1 7.1 -> 6.5 us, 1280@8^2 at batch
+// 2 39.2 -> 34.9 us); LDS-tiled otherwise, the tile chosen from a sweep of
+// every tile shape on MI355X
 // (GEMM launch alone, per-kernel events, min of 2 x 60 launches, us; the
 // results are bit-identical across tile shapes):
 //  * 128 x 128 for K >= 512 with BP >= 256 (512@7^2 B=64 17.1 vs 20.3-22.4
