@@ -390,16 +390,21 @@ int choose_path(const Handle* Hd, const Shape& s) {
     // at 28^2-56^2, C = 48 -> K = 40 at 13^2, NCHW and NHWC, batch 2-192;
     // the rule picks the faster path in all but 5, which lose 0.2-3 us):
     //  * fused tile-block: its workgroups run one per CU, so the time steps
-    //    by waves of workgroups over the CUs, ~3 us + 10 us per 32-channel
-    //    chunk each (conv2_x batch 16-36: 25.7-27.3 us, one wave; 40-72:
-    //    44-53 us; C = 32: 15 us per wave);
+    //    by waves of workgroups over the CUs: the staged (channels-last)
+    //    form ~3 us + 10 us per 32-channel chunk each wave (conv2_x batch
+    //    16-36: 25.7-27.3 us, one wave; 40-72: 44-53 us; C = 32: 15 us per
+    //    wave), the unstaged NCHW form ~3 us once + 9.6 us per chunk and
+    //    wave (conv2_x batch 8-36: 20.6-23.4 us; batch 40, 280 workgroups:
+    //    37.1; batch 64: 41.9; batch 128: 79.0; C = 32 batch 8-32: 11.7-12.6,
+    //    batch 64: 23.3);
     //  * three-pass: ~10 us of dependent launches plus its HBM bytes (x, y,
     //    V and M written and read) at 5 TB/s (conv2_x batch 16: 27.0 us,
     //    batch 128: 122 us).
-    // Examples, three-pass vs fused, us: conv2_x B=8 21.5 vs 25.2, B=16 27.0
-    // vs 25.7, B=44 46.7 vs 50.5, B=56 55.0 vs 51.4, B=112 102.8 vs 91.4;
-    // 64@28^2 B=64 29.1 vs 25.6; 32@56^2 B=8 19.7 vs 15.0; 48->40@13^2 B=128
-    // 22.8 vs 24.2.
+    // Examples, three-pass vs fused (unstaged form), us: conv2_x B=8 21.1 vs
+    // 20.6, B=16 27.4 vs 21.0, B=36 40.1 vs 23.4, B=40 41.6 vs 37.1; 64@28^2
+    // B=64 29.3 vs 21.3; 32@56^2 B=8 18.7 vs 11.7, B=64 42.5 vs 23.3;
+    // 64@112^2 B=8 33.4 vs 21.8, B=16 51.7 vs 41.5; 48->40@13^2 B=128 21.5
+    // vs 19.5.
     // Small problems (the small-problem kernel's grid at most two workgroups
     // per CU): one launch of that kernel. Measured on MI355X, us, three-pass
     // vs small kernel: conv2_x B=1 10.4 vs 7.5, B=2 12.0 vs 10.4 (B=4 16.9 vs
@@ -412,19 +417,25 @@ int choose_path(const Handle* Hd, const Shape& s) {
     FusedBlockPlan bp;
     if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
-        const double t_fused = (double)waves * (3.0 + 10.0 * ((Hd->Cp + 31) / 32));
+        const int chunks = (Hd->Cp + 31) / 32;
+        const double t_fused = Hd->nhwc ? (double)waves * (3.0 + 10.0 * chunks)
+                                         : 3.0 + (double)waves * 9.6 * chunks;
         const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
                            4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
         const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us
         // The two-pass path beats the tile-block kernel from two 32-channel
         // chunks up while its grid leaves a fifth of the CUs free (us,
-        // tile-block vs two-pass, NCHW / NHWC: 64@56^2 B=12 23.5 vs 18.8 /
-        // 24.6 vs 19.0, B=16 23.6 vs 19.9 / 25.0 vs 20.0; 64@28^2 B=48 23.1 vs
-        // 19.2 / 24.0 vs 18.6; 48@56^2 B=16 22.1 vs 18.0 / 24.7 vs 18.3;
-        // 64->48@28^2 B=32 22.0 vs 18.4 / 23.7 vs 17.6); not at one chunk
-        // (32@56^2 B=32 15.2 vs 18.5), and by little or not at all nearer a
-        // full round (250 workgroups: 64@56^2 B=20 23.8 vs 23.3, cold 29.8 vs
-        // 32.4; 64@28^2 B=80 23.8 vs 25.1).
+        // tile-block vs two-pass; NCHW, the unstaged form: 64@56^2 B=8 20.6
+        // vs 16.3, B=12 20.8 vs 18.7, B=16 21.0 vs 20.0; 64@28^2 B=32 20.9 vs
+        // 18.3, B=48 21.1 vs 19.1; 48@56^2 B=16 19.8 vs 17.7; 64->48@28^2
+        // B=32 19.8 vs 18.0; 48->40@13^2 B=128 19.5 vs 17.1; 64@112^2 B=2
+        // 20.5 vs 16.4, B=4 20.9 vs 20.2; NHWC, the staged form: 64@56^2
+        // B=12 24.6 vs 19.0, B=16 25.0 vs 20.0; 64@28^2 B=48 24.0 vs 18.6);
+        // not at one chunk (32@56^2 B=32 12.6 vs 18.6), nor from about 200
+        // two-pass workgroups on, where the two trade places by shape
+        // (64@28^2 B=64, 200: 21.3 vs 22.4; 64@224^2 B=1, 182: 20.9 vs 24.1;
+        // 64@56^2 B=20, 250: 21.3 vs 23.1; 48->40@13^2 B=192, 216: 19.9 vs
+        // 20.4).
         if (t_fused < t_three) {
             const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
             const bool two = Hd->Cp > 32 && 5 * grid <= 4 * (int64_t)Hd->cus && two_pass_wins(Hd, s);

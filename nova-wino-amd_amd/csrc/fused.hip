@@ -57,7 +57,7 @@ struct FusedArgs {
     _Float16* y;
     _Float16* Ms;
     unsigned* cnt;
-    int x_bytes;  // bytes from x_al to the end of x
+    int x_bytes;  // bytes from x_al through the dword holding the last element of x
     int xd;       // x - x_al in bytes
     int u_bytes, y_bytes;
     int C, K, Cp, H, W, pad, nh, nw, Ho, Wo;
@@ -464,7 +464,7 @@ hipError_t launch_fused(const uint16_t* x, const uint16_t* Uf, uint16_t* y, uint
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
     a.xd = (int)(xp & 15);
-    a.x_bytes = (int)(2 * (int64_t)B * C * H * W + a.xd);
+    a.x_bytes = (int)dword_ceil(2 * (int64_t)B * C * H * W + a.xd);
     a.Uf = reinterpret_cast<const _Float16*>(Uf);
     a.u_bytes = (int)(2 * u_frag_elems(K, Cp));
     a.y = reinterpret_cast<_Float16*>(y);

@@ -26,6 +26,11 @@
 //     and every thread runs the output transform for 2 (k, tile) pairs.
 // The transforms are the shared tile arithmetic (bit-identical to the
 // standalone kernels); products accumulate over 32-channel chunks in order.
+// That staged form (fused_block_kernel) serves channels-last tensors and,
+// when forced, NCHW layers above 64 input channels; NCHW layers with at most
+// 64 take fused_block_kernel_direct below: the same workgroup and arithmetic, no
+// staging (patch rows loaded straight into registers, V of both chunks
+// built in one pass), so y is the same bit for bit.
 #include <algorithm>
 #include <type_traits>
 
@@ -103,6 +108,67 @@ constexpr int kNhwcPix = 36;  // 72 bytes: tiles 6 pixels apart fall in distinct
 // and the MFMA write, with lanes over tiles, at a 16-byte offset per tile.
 constexpr int kNhwcTileP = 64 * 72 + 8;
 static_assert(16 * kNhwcTileP * 2 <= 160 * 1024, "NHWC M fits in LDS");
+
+// Output phase of the NCHW forms: thread (kk, tile t) pairs e = tid + 512 i,
+// M read as 8 16-byte rows of [kk][tile][position], the output transform,
+// epilogue and residual, 4-byte pair stores where y allows them.
+template <bool kEpi>
+__device__ __forceinline__ void output_phase_nchw(const BlockArgs& a, const _Float16* ms, int tid,
+                                                  int t, bool tile_ok, int th, int tw, int b,
+                                                  int k0, __amdgpu_buffer_rsrc_t yrs) {
+    const bool pairs_w = a.y_pairs != 0;
+    const _Float16* res = a.residual;
+    const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
+    const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
+    for (int e = tid; e < 64 * 16; e += kBT) {
+        const int kk = e >> 4;
+        const int k = k0 + kk;
+        if (!tile_ok || k >= a.K) continue;
+        h8 mv[8];
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++)
+            mv[ii] = *reinterpret_cast<const h8*>(ms + (kk * 16 + t) * kBMPitch + 8 * ii);
+        float out[6][6];
+        output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
+        const int oh = th * 6, ow = tw * 6;
+        const int ybase = 2 * ((b * a.K + k) * a.Ho * a.Wo + ow);
+        const ChannelEpilogue<kEpi> epi(a.bias, k, relu0);
+#pragma unroll
+        for (int r = 0; r < 6; r++) {
+            const int row = ybase + 2 * (oh + r) * a.Wo;
+            if (oh + r >= a.Ho) break;
+            if (pairs_w) {
+#pragma unroll
+                for (int s = 0; s < 6; s += 2) {
+                    if (ow + s < a.Wo) {
+                        const unsigned lo = __builtin_bit_cast(uint16_t, epi(out[r][s]));
+                        const unsigned hi = __builtin_bit_cast(uint16_t, epi(out[r][s + 1]));
+                        unsigned v = lo | (hi << 16);
+                        if (res)
+                            v = add_residual2(
+                                v, __builtin_amdgcn_raw_buffer_load_b32(rrs, row + 2 * s, 0, 0),
+                                a.relu);
+                        __builtin_amdgcn_raw_buffer_store_b32(v, yrs, row + 2 * s, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < 6; s++)
+                    if (ow + s < a.Wo) {
+                        _Float16 v = epi(out[r][s]);
+                        if (res)
+                            v = add_residual(
+                                v,
+                                __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
+                                                                 rrs, row + 2 * s, 0, 0)),
+                                a.relu);
+                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
+                                                              row + 2 * s, 0, 0);
+                    }
+            }
+        }
+    }
+}
 
 template <int NJ, bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
@@ -343,11 +409,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     __syncthreads();
 
     // ---- output transform: (kk, tile) pairs, tile = tid % 16 ----
-    const bool pairs_w = a.y_pairs != 0;
-    const _Float16* res = a.residual;
-    const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
-    const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
     if constexpr (kNhwc) {
+        const _Float16* res = a.residual;
+        const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
+        const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
         // lanes over channels: pair e = (tile e / 64, channel e % 64)
         for (int e = tid; e < 64 * 16; e += kBT) {
             const int kk = e & 63, to = e >> 6;
@@ -383,54 +448,212 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
         }
         return;
     }
-    for (int e = tid; e < 64 * 16; e += kBT) {
-        const int kk = e >> 4;
-        const int k = k0 + kk;
-        if (!tile_ok || k >= a.K) continue;
-        h8 mv[8];
+    output_phase_nchw<kEpi>(a, ms, tid, t, tile_ok, th, tw, b, k0, yrs);
+}
+
+// ---------------------------------------------------------------------------
+// NCHW form for Cp <= 64 (NS = 1 or 2 steps of 32 channels): no staging.
+// Same workgroup (16 tiles x 64 output channels x 64 positions, 8 waves)
+// and the same arithmetic in the same order, so y equals the staged form's
+// bit for bit; the phases are re-planned around the register budget:
+//   * every thread loads the 8 rows of its NS patches (channel ct + 32 j,
+//     tile t) straight from global memory, each row as a 16-byte and a
+//     4-byte load from the dword at or below its start, all NS*16 loads in
+//     flight at once; no LDS holds the input, so V for all NS steps (NS KB
+//     per position) fits beside nothing else and is built in one pass;
+//   * no accumulator lives during the transform, so the U operands of the
+//     wave's first kPreU positions (both steps) are requested before it and
+//     arrive during its VALU work;
+//   * each wave then finishes one position at a time (both steps, the first
+//     MFMA from a zero accumulator), requesting the next position's
+//     operands as registers free up;
+//   * after a barrier, M is written over V ([k][tile][position], as the
+//     staged form) and the output phase is the staged form's.
+// Rows that start before x_al (only the first row of channel 0 of image 0
+// with left padding and a 16-byte aligned x) are loaded from offset 0 and
+// shifted into place in a branch that only the wave holding them takes.
+// ---------------------------------------------------------------------------
+constexpr int kPreU = 3;  // positions whose U operands are requested before the transform
+
+template <int NS, bool kEpi>
+__global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a) {
+    static_assert(NS == 1 || NS == 2, "one or two 32-channel steps");
+    static_assert(64 * kBMPitch * 16 * 2 <= kBLdsBytes, "M fits in LDS");
+    __shared__ __align__(16) unsigned char lds[kBLdsBytes];
+    _Float16* vs = reinterpret_cast<_Float16*>(lds);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = position row
+
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int kblk = L % a.n_kblk;
+    const int rest = L / a.n_kblk;
+    const int run = rest % a.nruns;
+    const int b = rest / a.nruns;
+    const int k0 = kblk * 64;
+    const int t0 = run * 16;
+    const int ntiles = min(16, a.P - t0);
+    const int HW = a.H * a.W;
+    const __amdgpu_buffer_rsrc_t xrs = rsrc(a.x_al, a.x_bytes);
+    const __amdgpu_buffer_rsrc_t urs = rsrc(a.U, a.u_bytes);
+    const __amdgpu_buffer_rsrc_t yrs = rsrc(a.y, a.y_bytes);
+
+    // ---- transform role: channel ct + 32 j (j < NS), tile t ----
+    const int t = tid & 15;
+    const int ct = tid >> 4;
+    const bool tile_ok = t < ntiles;
+    const int tl = t0 + (tile_ok ? t : 0);
+    const int th = tl / a.nw, tw = tl - (tl / a.nw) * a.nw;
+    const int h0 = 6 * th - a.pad, w0 = 6 * tw - a.pad;
+    unsigned cmask = 0;
 #pragma unroll
-        for (int ii = 0; ii < 8; ii++)
-            mv[ii] = *reinterpret_cast<const h8*>(ms + (kk * 16 + t) * kBMPitch + 8 * ii);
-        float out[6][6];
-        output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
-        const int oh = th * 6, ow = tw * 6;
-        const int ybase = 2 * ((b * a.K + k) * a.Ho * a.Wo + ow);
-        const ChannelEpilogue<kEpi> epi(a.bias, k, relu0);
+    for (int ii = 0; ii < 8; ii++) {
+        const int w = w0 + ii;
+        cmask |= (w >= 0 && w < a.W) ? (1u << ii) : 0u;
+    }
+    unsigned dm[4];
 #pragma unroll
-        for (int r = 0; r < 6; r++) {
-            const int row = ybase + 2 * (oh + r) * a.Wo;
-            if (oh + r >= a.Ho) break;
-            if (pairs_w) {
+    for (int q = 0; q < 4; q++)
+        dm[q] = (((cmask >> (2 * q)) & 1u) ? 0xffffu : 0u) |
+                (((cmask >> (2 * q + 1)) & 1u) ? 0xffff0000u : 0u);
+
+    // ---- patch rows: 20 bytes from the dword at or below the row start ----
+    // (rows outside the image, channels past C and empty tile slots read
+    // zeros through out-of-range offsets)
+    unsigned w5[NS][8][5];
+    unsigned odd[NS], neg[NS];  // per row: start at a 2-byte offset; start before x_al
 #pragma unroll
-                for (int s = 0; s < 6; s += 2) {
-                    if (ow + s < a.Wo) {
-                        const unsigned lo = __builtin_bit_cast(uint16_t, epi(out[r][s]));
-                        const unsigned hi = __builtin_bit_cast(uint16_t, epi(out[r][s + 1]));
-                        unsigned v = lo | (hi << 16);
-                        if (res)
-                            v = add_residual2(
-                                v, __builtin_amdgcn_raw_buffer_load_b32(rrs, row + 2 * s, 0, 0),
-                                a.relu);
-                        __builtin_amdgcn_raw_buffer_store_b32(v, yrs, row + 2 * s, 0, 0);
-                    }
+    for (int j = 0; j < NS; j++) {
+        const int c = ct + 32 * j;
+        odd[j] = 0;
+        neg[j] = 0;
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) {
+            const int h = h0 + ii;
+            const bool ok = tile_ok && c < a.C && h >= 0 && h < a.H;
+            const int o = a.xd + 2 * ((b * a.C + c) * HW + h * a.W + w0);
+            odd[j] |= (unsigned)((o >> 1) & 1) << ii;
+            neg[j] |= (ok && o < 0) ? (1u << ii) : 0u;
+            const int A = !ok ? kBOob : (o < 0 ? 0 : (o & ~3));
+            const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, A, 0, 0);
+#pragma unroll
+            for (int q = 0; q < 4; q++) w5[j][ii][q] = v[q];
+            w5[j][ii][4] = __builtin_amdgcn_raw_buffer_load_b32(xrs, A + 16, 0, 0);
+        }
+    }
+
+    // ---- U operands of this wave's first kPreU positions, both steps ----
+    h8 ua[8][4][NS];
+    auto load_u = [&](int s) {
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int j = 0; j < NS; j++)
+                ua[s][kb][j] = __builtin_bit_cast(
+                    h8, __builtin_amdgcn_raw_buffer_load_b128(
+                            urs, lane * 16, u_off(a, 8 * wave + s, k0 / 16 + kb, j), 0));
+    };
+#pragma unroll
+    for (int s = 0; s < kPreU; s++) load_u(s);
+
+    // a row that starts before x_al was loaded from offset 0: move its dwords
+    // up by the missing ones (zeros before the buffer, all in masked columns)
+    unsigned any_neg = 0;
+#pragma unroll
+    for (int j = 0; j < NS; j++) any_neg |= neg[j];
+    if (__builtin_amdgcn_ballot_w64(any_neg != 0) != 0) {
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            const int c = ct + 32 * j;
+#pragma unroll
+            for (int ii = 0; ii < 8; ii++) {
+                if (!((neg[j] >> ii) & 1u)) continue;
+                const int o = a.xd + 2 * ((b * a.C + c) * HW + (h0 + ii) * a.W + w0);
+                const int sh = -(o >> 2);  // dwords before x_al (o >> 2 rounds down)
+                unsigned l5[5];
+#pragma unroll
+                for (int q = 0; q < 5; q++) l5[q] = w5[j][ii][q];
+#pragma unroll
+                for (int q = 0; q < 5; q++) {
+                    unsigned v = 0;
+#pragma unroll
+                    for (int r = 0; r < 5; r++) v = (q - sh == r) ? l5[r] : v;
+                    w5[j][ii][q] = v;
                 }
-            } else {
-#pragma unroll
-                for (int s = 0; s < 6; s++)
-                    if (ow + s < a.Wo) {
-                        _Float16 v = epi(out[r][s]);
-                        if (res)
-                            v = add_residual(
-                                v,
-                                __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
-                                                                 rrs, row + 2 * s, 0, 0)),
-                                a.relu);
-                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
-                                                              row + 2 * s, 0, 0);
-                    }
             }
         }
     }
+
+    // ---- input transform of the NS patches into V: [position][step][the
+    // staged form's 1 KB operand block] ----
+#pragma unroll
+    for (int j = 0; j < NS; j++) {
+        unsigned d4[8][4];
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++) {
+            const unsigned sb = ((odd[j] >> ii) & 1u) * 2;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                d4[ii][q] = __builtin_amdgcn_alignbyte(w5[j][ii][q + 1], w5[j][ii][q], sb);
+        }
+        if (cmask != 0xffu) {
+#pragma unroll
+            for (int ii = 0; ii < 8; ii++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) d4[ii][q] &= dm[q];
+        }
+        _Float16* vj = vs + j * 512;
+        input_tile_rows(
+            [&](int ii, int jj) {
+                const unsigned pr = d4[ii][jj >> 1];
+                const unsigned short bits =
+                    (unsigned short)((jj & 1) ? (pr >> 16) : (pr & 0xffffu));
+                return (float)__builtin_bit_cast(_Float16, bits);
+            },
+            [&](int r, int s2, float v) {
+                vj[(r * 8 + s2) * (NS * 512) + v_index(0, ct, t)] = to_f16(v);
+            });
+    }
+    __syncthreads();
+
+    // ---- products: one position at a time, both steps in channel order ----
+    f4 acc[8][4];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int pos = 8 * wave + s;
+        h8 vb[NS];
+#pragma unroll
+        for (int j = 0; j < NS; j++)
+            vb[j] = *reinterpret_cast<const h8*>(vs + pos * (NS * 512) + j * 512 + lane * 8);
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                ua[s][kb][0], vb[0], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            if constexpr (NS == 2)
+                acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[s][kb][1], vb[1],
+                                                                    acc[s][kb], 0, 0, 0);
+        }
+        if (s + kPreU < 8) load_u(s + kPreU);
+    }
+    __syncthreads();  // V becomes M
+
+    // ---- M (fp16) to LDS: [kk][tile][position], as the staged form ----
+    _Float16* ms = reinterpret_cast<_Float16*>(lds);
+    {
+        const int g = lane >> 4, tq = lane & 15;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kk = 16 * kb + 4 * g + i;
+                h8 v;
+#pragma unroll
+                for (int s = 0; s < 8; s++) v[s] = to_f16(acc[s][kb][i]);
+                *reinterpret_cast<h8*>(ms + (kk * 16 + tq) * kBMPitch + 8 * wave) = v;
+            }
+    }
+    __syncthreads();
+    output_phase_nchw<kEpi>(a, ms, tid, t, tile_ok, th, tw, b, k0, yrs);
 }
 
 int round16i(int v) { return (v + 15) & ~15; }
@@ -439,7 +662,6 @@ int round16i(int v) { return (v + 15) & ~15; }
 
 bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
                       FusedBlockPlan* p, bool nhwc) {
-    (void)Cp;
     if (B < 1 || C < 1 || K < 1) return false;
     const int P = nh * nw;
     const int nruns = (P + 15) / 16;
@@ -456,6 +678,9 @@ bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
         if (C % 8 != 0 || rows_st * cols * kNhwcPix * 2 > kBXBytes) return false;
         p->cols = cols;
         p->rp = p->cp = p->nj = 0;
+    } else if (Cp <= 64) {
+        // the unstaged form (fused_block_kernel_direct): no limit on the image width
+        p->cols = p->rp = p->cp = p->nj = 0;
     } else {
         const int rp = round16i(2 * (6 * nw + 2) + 18);
         const int cp = rows_st * rp + 16;
@@ -483,7 +708,7 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     a.x_al = reinterpret_cast<const void*>(xp & ~(uintptr_t)15);
     a.xd = (int)(xp & 15);
-    a.x_bytes = (int)(2 * (int64_t)B * C * H * W + a.xd);
+    a.x_bytes = (int)dword_ceil(2 * (int64_t)B * C * H * W + a.xd);
     a.U = reinterpret_cast<const _Float16*>(U);
     a.u_bytes = (int)(2 * u_frag_elems(K, Cp));
     a.nkt = (K + 15) / 16;
@@ -519,6 +744,13 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     if (p.nhwc) {
         if (a.xd != 0) return hipErrorInvalidValue;  // 16-byte loads need an aligned x
         epi ? go(fused_block_kernel<0, true, true>) : go(fused_block_kernel<0, true, false>);
+        return hipGetLastError();
+    }
+    if (Cp <= 64) {
+        if (Cp > 32)
+            epi ? go(fused_block_kernel_direct<2, true>) : go(fused_block_kernel_direct<2, false>);
+        else
+            epi ? go(fused_block_kernel_direct<1, true>) : go(fused_block_kernel_direct<1, false>);
         return hipGetLastError();
     }
     auto go_nj = [&](auto nj) {

@@ -60,6 +60,14 @@ inline int tiles_min(int out) { return (out + 5) / 6; }
 // Pad a channel count to the 8-element (16-byte) granule of the GEMM loads.
 inline int pad8(int c) { return (c + 7) & ~7; }
 
+// Size of a buffer resource over an fp16 tensor read with loads of 4 bytes or
+// more: a raw buffer load returns zero for a whole dword that extends past
+// the resource's size (measured on MI355X: with 2 mod 4 bytes the tensor's
+// last element read as zero), so the size is rounded up to the dword that
+// holds the last element. The bytes added share that dword, hence its page;
+// the kernels mask the columns they land in.
+inline int64_t dword_ceil(int64_t bytes) { return (bytes + 3) & ~(int64_t)3; }
+
 // ---- filter transform ----------------------------------------------------
 // Reference layout: U[p][c][k] (U[p*K*C + c*K + k]).
 hipError_t launch_filter_transform_ref(const float* w, uint16_t* U, int K, int C,

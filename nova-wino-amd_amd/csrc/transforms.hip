@@ -577,7 +577,7 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     // so no byte outside x's pages is touched); offsets stay 32-bit.
     const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
     const int xd = (int)(xp & 15);
-    const int64_t x_bytes = 2 * (int64_t)B * C * H * W + xd;
+    const int64_t x_bytes = dword_ceil(2 * (int64_t)B * C * H * W + xd);
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
     auto go = [&](auto kernel) {
