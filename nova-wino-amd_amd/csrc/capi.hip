@@ -393,10 +393,9 @@ int choose_path(const Handle* Hd, const Shape& s) {
     //    by waves of workgroups over the CUs: the staged (channels-last)
     //    form ~3 us + 10 us per 32-channel chunk each wave (conv2_x batch
     //    16-36: 25.7-27.3 us, one wave; 40-72: 44-53 us; C = 32: 15 us per
-    //    wave), the unstaged NCHW form ~3 us once + 9.6 us per chunk and
-    //    wave (conv2_x batch 8-36: 20.6-23.4 us; batch 40, 280 workgroups:
-    //    37.1; batch 64: 41.9; batch 128: 79.0; C = 32 batch 8-32: 11.7-12.6,
-    //    batch 64: 23.3);
+    //    wave), the unstaged NCHW form ~3 us once + 9.2 us per chunk and
+    //    wave (conv2_x batch 16: 20.4 us, 32: 21.4, 128: 76.5; C = 32 batch
+    //    32: 12.5, 64: 23.2; 64@112^2 batch 8: 21.2);
     //  * three-pass: ~10 us of dependent launches plus its HBM bytes (x, y,
     //    V and M written and read) at 5 TB/s (conv2_x batch 16: 27.0 us,
     //    batch 128: 122 us).
@@ -419,7 +418,7 @@ int choose_path(const Handle* Hd, const Shape& s) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
         const int chunks = (Hd->Cp + 31) / 32;
         const double t_fused = Hd->nhwc ? (double)waves * (3.0 + 10.0 * chunks)
-                                         : 3.0 + (double)waves * 9.6 * chunks;
+                                         : 3.0 + (double)waves * 9.2 * chunks;
         const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
                            4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
         const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us

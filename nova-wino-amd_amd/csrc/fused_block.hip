@@ -462,8 +462,9 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 //     flight at once; no LDS holds the input, so V for all NS steps (NS KB
 //     per position) fits beside nothing else and is built in one pass;
 //   * no accumulator lives during the transform, so the U operands of the
-//     wave's first kPreU positions (both steps) are requested before it and
-//     arrive during its VALU work;
+//     wave's first kPreU positions (both steps) are requested before it, and
+//     of kMidU more once the first of two patches is transformed (its
+//     registers are free then); they arrive during the VALU work;
 //   * each wave then finishes one position at a time (both steps, the first
 //     MFMA from a zero accumulator), requesting the next position's
 //     operands as registers free up;
@@ -473,7 +474,13 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 // with left padding and a 16-byte aligned x) are loaded from offset 0 and
 // shifted into place in a branch that only the wave holding them takes.
 // ---------------------------------------------------------------------------
-constexpr int kPreU = 3;  // positions whose U operands are requested before the transform
+// Positions whose U operands are requested before the transform (one step:
+// 6; two steps: 3, and kMidU more once the first patch is transformed).
+// Whole forwards, graph of ten, us: conv2_x B=32 22.25 (3 before) -> 21.43
+// (3 + 3), B=128 78.7 -> 76.5; C = 32 B=32 12.75 (3) -> 12.49 (6).
+template <int NS>
+constexpr int kPreU = NS == 1 ? 6 : 3;
+constexpr int kMidU = 3;
 
 template <int NS, bool kEpi>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a) {
@@ -554,7 +561,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                             urs, lane * 16, u_off(a, 8 * wave + s, k0 / 16 + kb, j), 0));
     };
 #pragma unroll
-    for (int s = 0; s < kPreU; s++) load_u(s);
+    for (int s = 0; s < kPreU<NS>; s++) load_u(s);
 
     // a row that starts before x_al was loaded from offset 0: move its dwords
     // up by the missing ones (zeros before the buffer, all in masked columns)
@@ -602,6 +609,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
 #pragma unroll
                 for (int q = 0; q < 4; q++) d4[ii][q] &= dm[q];
         }
+        if (j == 1) {
+#pragma unroll
+            for (int s = kPreU<NS>; s < kPreU<NS> + kMidU; s++) load_u(s);
+        }
         _Float16* vj = vs + j * 512;
         input_tile_rows(
             [&](int ii, int jj) {
@@ -633,7 +644,8 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                 acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[s][kb][1], vb[1],
                                                                     acc[s][kb], 0, 0, 0);
         }
-        if (s + kPreU < 8) load_u(s + kPreU);
+        constexpr int kAhead = kPreU<NS> + (NS == 2 ? kMidU : 0);  // positions already requested
+        if (s + kAhead < 8) load_u(s + kAhead);
     }
     __syncthreads();  // V becomes M
 
