@@ -389,13 +389,12 @@ int choose_path(const Handle* Hd, const Shape& s) {
     // by a cost model fitted to MI355X forwards (36 shapes: C = K = 32 and 64
     // at 28^2-56^2, C = 48 -> K = 40 at 13^2, NCHW and NHWC, batch 2-192;
     // the rule picks the faster path in all but 5, which lose 0.2-3 us):
-    //  * fused tile-block: its workgroups run one per CU, so the time steps
-    //    by waves of workgroups over the CUs: the staged (channels-last)
-    //    form ~3 us + 10 us per 32-channel chunk each wave (conv2_x batch
-    //    16-36: 25.7-27.3 us, one wave; 40-72: 44-53 us; C = 32: 15 us per
-    //    wave), the unstaged NCHW form ~3 us once + 9.2 us per chunk and
-    //    wave (conv2_x batch 16: 20.4 us, 32: 21.4, 128: 76.5; C = 32 batch
-    //    32: 12.5, 64: 23.2; 64@112^2 batch 8: 21.2);
+    //  * fused tile-block (its unstaged form, both layouts): its workgroups
+    //    run one per CU, so the time steps by waves of workgroups over the
+    //    CUs, ~3 us once + 9.2 us per 32-channel chunk and wave (conv2_x
+    //    batch 16: 20.4 us, 32: 21.4, 128: 76.5; C = 32 batch 32: 12.5, 64:
+    //    23.2; 64@112^2 batch 8: 21.2; channels-last conv2_x batch 16: 21.0,
+    //    32: 21.9, 128: 78.6, C = 32 batch 32: 16.0);
     //  * three-pass: ~10 us of dependent launches plus its HBM bytes (x, y,
     //    V and M written and read) at 5 TB/s (conv2_x batch 16: 27.0 us,
     //    batch 128: 122 us).
@@ -417,8 +416,7 @@ int choose_path(const Handle* Hd, const Shape& s) {
     if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
         const int chunks = (Hd->Cp + 31) / 32;
-        const double t_fused = Hd->nhwc ? (double)waves * (3.0 + 10.0 * chunks)
-                                         : 3.0 + (double)waves * 9.2 * chunks;
+        const double t_fused = 3.0 + (double)waves * 9.2 * chunks;
         const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
                            4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
         const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us
@@ -598,7 +596,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     }
     int path = choose_path(Hd, s_all);
     // the channels-last tile-block kernel stages x with 16-byte loads
-    if (path == 3 && Hd->nhwc && !aligned16(x)) path = 1;
+    // (the staged channels-last form, above 64 channels, loads 16 bytes at a time)
+    if (path == 3 && Hd->nhwc && Hd->Cp > 64 && !aligned16(x)) path = 1;
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s_all));
     if (no_alloc) {
         // the position-row kernel needs an allocated M buffer and counters,

@@ -26,10 +26,10 @@
 //     and every thread runs the output transform for 2 (k, tile) pairs.
 // The transforms are the shared tile arithmetic (bit-identical to the
 // standalone kernels); products accumulate over 32-channel chunks in order.
-// That staged form (fused_block_kernel) serves channels-last tensors and,
-// when forced, NCHW layers above 64 input channels; NCHW layers with at most
-// 64 take fused_block_kernel_direct below: the same workgroup and arithmetic, no
-// staging (patch rows loaded straight into registers, V of both chunks
+// That staged form (fused_block_kernel) serves layers above 64 input
+// channels, when forced; layers with at most 64, NCHW and channels-last,
+// take fused_block_kernel_direct below: the same workgroup and arithmetic,
+// no staging (patch rows loaded straight into registers, V of both chunks
 // built in one pass), so y is the same bit for bit.
 #include <algorithm>
 #include <type_traits>
@@ -166,6 +166,51 @@ __device__ __forceinline__ void output_phase_nchw(const BlockArgs& a, const _Flo
                                                               row + 2 * s, 0, 0);
                     }
             }
+        }
+    }
+}
+
+// Output phase of the channels-last forms: lanes over 64 consecutive output
+// channels (pair e = (tile e / 64, channel e % 64)), M read as 8 16-byte rows
+// of [tile][kk][position], 2-byte NHWC stores (128 bytes per wave and pixel).
+template <bool kEpi>
+__device__ __forceinline__ void output_phase_nhwc(const BlockArgs& a, const _Float16* ms, int tid,
+                                                  int ntiles, int t0, int b, int k0,
+                                                  __amdgpu_buffer_rsrc_t yrs) {
+    const _Float16* res = a.residual;
+    const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
+    const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
+    // lanes over channels: pair e = (tile e / 64, channel e % 64)
+    for (int e = tid; e < 64 * 16; e += kBT) {
+        const int kk = e & 63, to = e >> 6;
+        const int k = k0 + kk;
+        if (to >= ntiles || k >= a.K) continue;
+        h8 mv[8];
+#pragma unroll
+        for (int ii = 0; ii < 8; ii++)
+            mv[ii] = *reinterpret_cast<const h8*>(ms + to * kNhwcTileP + kk * kBMPitch + 8 * ii);
+        float out[6][6];
+        output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
+        const int tlo = t0 + to;
+        const int oh = (tlo / a.nw) * 6, ow = (tlo - (tlo / a.nw) * a.nw) * 6;
+        const ChannelEpilogue<kEpi> epi(a.bias, k, relu0);
+#pragma unroll
+        for (int r = 0; r < 6; r++) {
+            if (oh + r >= a.Ho) break;
+#pragma unroll
+            for (int s = 0; s < 6; s++)
+                if (ow + s < a.Wo) {
+                    const int off = 2 * (((b * a.Ho + oh + r) * a.Wo + ow + s) * a.K + k);
+                    _Float16 v = epi(out[r][s]);
+                    if (res)
+                        v = add_residual(
+                            v,
+                            __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
+                                                             rrs, off, 0, 0)),
+                            a.relu);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
+                                                          off, 0, 0);
+                }
         }
     }
 }
@@ -410,57 +455,26 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 
     // ---- output transform: (kk, tile) pairs, tile = tid % 16 ----
     if constexpr (kNhwc) {
-        const _Float16* res = a.residual;
-        const int relu0 = res ? 0 : a.relu;  // with a residual the ReLU comes after it
-        const __amdgpu_buffer_rsrc_t rrs = rsrc(res, res ? a.y_bytes : 0);
-        // lanes over channels: pair e = (tile e / 64, channel e % 64)
-        for (int e = tid; e < 64 * 16; e += kBT) {
-            const int kk = e & 63, to = e >> 6;
-            const int k = k0 + kk;
-            if (to >= ntiles || k >= a.K) continue;
-            h8 mv[8];
-#pragma unroll
-            for (int ii = 0; ii < 8; ii++)
-                mv[ii] = *reinterpret_cast<const h8*>(ms + to * kNhwcTileP + kk * kBMPitch + 8 * ii);
-            float out[6][6];
-            output_tile([&](int ii, int j) { return (float)mv[ii][j]; }, out);
-            const int tlo = t0 + to;
-            const int oh = (tlo / a.nw) * 6, ow = (tlo - (tlo / a.nw) * a.nw) * 6;
-            const ChannelEpilogue<kEpi> epi(a.bias, k, relu0);
-#pragma unroll
-            for (int r = 0; r < 6; r++) {
-                if (oh + r >= a.Ho) break;
-#pragma unroll
-                for (int s = 0; s < 6; s++)
-                    if (ow + s < a.Wo) {
-                        const int off = 2 * (((b * a.Ho + oh + r) * a.Wo + ow + s) * a.K + k);
-                        _Float16 v = epi(out[r][s]);
-                        if (res)
-                            v = add_residual(
-                                v,
-                                __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
-                                                                 rrs, off, 0, 0)),
-                                a.relu);
-                        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, v), yrs,
-                                                              off, 0, 0);
-                    }
-            }
-        }
+        output_phase_nhwc<kEpi>(a, ms, tid, ntiles, t0, b, k0, yrs);
         return;
     }
     output_phase_nchw<kEpi>(a, ms, tid, t, tile_ok, th, tw, b, k0, yrs);
 }
 
 // ---------------------------------------------------------------------------
-// NCHW form for Cp <= 64 (NS = 1 or 2 steps of 32 channels): no staging.
+// Unstaged form for Cp <= 64 (NS = 1 or 2 steps of 32 channels), NCHW and
+// channels-last (kNhwc: one 2-byte load per pixel, lanes over 32 channels of
+// 2 tiles, so a load covers 64 bytes of consecutive channels; any C and any
+// alignment of x).
 // Same workgroup (16 tiles x 64 output channels x 64 positions, 8 waves)
 // and the same arithmetic in the same order, so y equals the staged form's
 // bit for bit; the phases are re-planned around the register budget:
-//   * every thread loads the 8 rows of its NS patches (channel ct + 32 j,
-//     tile t) straight from global memory, each row as a 16-byte and a
+//   * every thread loads its NS patches (channel ct + 32 j, tile t)
+//     straight from global memory -- NCHW each row as a 16-byte and a
 //     4-byte load from the dword at or below its start, all NS*16 loads in
-//     flight at once; no LDS holds the input, so V for all NS steps (NS KB
-//     per position) fits beside nothing else and is built in one pass;
+//     flight at once -- so no LDS holds the input, and V for all NS steps
+//     (NS KB per position) fits beside nothing else and is built in one
+//     pass;
 //   * no accumulator lives during the transform, so the U operands of the
 //     wave's first kPreU positions (both steps) are requested before it, and
 //     of kMidU more once the first of two patches is transformed (its
@@ -468,24 +482,27 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 //   * each wave then finishes one position at a time (both steps, the first
 //     MFMA from a zero accumulator), requesting the next position's
 //     operands as registers free up;
-//   * after a barrier, M is written over V ([k][tile][position], as the
-//     staged form) and the output phase is the staged form's.
+//   * after a barrier, M is written over V (as the staged form lays it out
+//     for the layout) and the output phase is the staged form's.
 // Rows that start before x_al (only the first row of channel 0 of image 0
 // with left padding and a 16-byte aligned x) are loaded from offset 0 and
 // shifted into place in a branch that only the wave holding them takes.
 // ---------------------------------------------------------------------------
 // Positions whose U operands are requested before the transform (one step:
-// 6; two steps: 3, and kMidU more once the first patch is transformed).
+// 6; two steps: 3, and kMidU more once the first patch is transformed: 3,
+// or 2 channels-last, whose packed patch pairs leave fewer registers).
 // Whole forwards, graph of ten, us: conv2_x B=32 22.25 (3 before) -> 21.43
 // (3 + 3), B=128 78.7 -> 76.5; C = 32 B=32 12.75 (3) -> 12.49 (6).
 template <int NS>
 constexpr int kPreU = NS == 1 ? 6 : 3;
-constexpr int kMidU = 3;
+template <bool kNhwc>
+constexpr int kMidU = kNhwc ? 2 : 3;
 
-template <int NS, bool kEpi>
+template <int NS, bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a) {
     static_assert(NS == 1 || NS == 2, "one or two 32-channel steps");
-    static_assert(64 * kBMPitch * 16 * 2 <= kBLdsBytes, "M fits in LDS");
+    static_assert(64 * kBMPitch * 16 * 2 <= kBLdsBytes && 16 * kNhwcTileP * 2 <= kBLdsBytes,
+                  "M fits in LDS");
     __shared__ __align__(16) unsigned char lds[kBLdsBytes];
     _Float16* vs = reinterpret_cast<_Float16*>(lds);
     const int tid = threadIdx.x;
@@ -505,9 +522,12 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
     const __amdgpu_buffer_rsrc_t urs = rsrc(a.U, a.u_bytes);
     const __amdgpu_buffer_rsrc_t yrs = rsrc(a.y, a.y_bytes);
 
-    // ---- transform role: channel ct + 32 j (j < NS), tile t ----
-    const int t = tid & 15;
-    const int ct = tid >> 4;
+    // ---- transform role: channel ct + 32 j (j < NS), tile t. NCHW: a wave
+    // holds 16 tiles x 4 channels (a row load spans the 16 tiles of one
+    // channel); channels-last: 32 channels x 2 tiles (a pixel load spans 64
+    // bytes of consecutive channels) ----
+    const int t = kNhwc ? tid >> 5 : tid & 15;
+    const int ct = kNhwc ? tid & 31 : tid >> 4;
     const bool tile_ok = t < ntiles;
     const int tl = t0 + (tile_ok ? t : 0);
     const int th = tl / a.nw, tw = tl - (tl / a.nw) * a.nw;
@@ -527,25 +547,49 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
     // ---- patch rows: 20 bytes from the dword at or below the row start ----
     // (rows outside the image, channels past C and empty tile slots read
     // zeros through out-of-range offsets)
-    unsigned w5[NS][8][5];
+    unsigned w5[NS][8][5];      // NCHW: the five dwords of each row
+    unsigned px[NS][8][4];      // channels-last: the patch, column pairs packed
     unsigned odd[NS], neg[NS];  // per row: start at a 2-byte offset; start before x_al
 #pragma unroll
     for (int j = 0; j < NS; j++) {
         const int c = ct + 32 * j;
         odd[j] = 0;
         neg[j] = 0;
+        if constexpr (kNhwc) {
+            // one 2-byte load per pixel; pixels outside the image read zero
 #pragma unroll
-        for (int ii = 0; ii < 8; ii++) {
-            const int h = h0 + ii;
-            const bool ok = tile_ok && c < a.C && h >= 0 && h < a.H;
-            const int o = a.xd + 2 * ((b * a.C + c) * HW + h * a.W + w0);
-            odd[j] |= (unsigned)((o >> 1) & 1) << ii;
-            neg[j] |= (ok && o < 0) ? (1u << ii) : 0u;
-            const int A = !ok ? kBOob : (o < 0 ? 0 : (o & ~3));
-            const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, A, 0, 0);
+            for (int ii = 0; ii < 8; ii++) {
+                const int h = h0 + ii;
+                const bool rok = tile_ok && c < a.C && h >= 0 && h < a.H;
 #pragma unroll
-            for (int q = 0; q < 4; q++) w5[j][ii][q] = v[q];
-            w5[j][ii][4] = __builtin_amdgcn_raw_buffer_load_b32(xrs, A + 16, 0, 0);
+                for (int q = 0; q < 4; q++) {
+                    unsigned pr = 0;
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int w = w0 + 2 * q + e;
+                        const bool ok = rok && w >= 0 && w < a.W;
+                        const int o = a.xd + 2 * (((b * a.H + h) * a.W + w) * a.C + c);
+                        pr |= (unsigned)__builtin_amdgcn_raw_buffer_load_b16(xrs, ok ? o : kBOob,
+                                                                             0, 0)
+                              << (16 * e);
+                    }
+                    px[j][ii][q] = pr;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ii = 0; ii < 8; ii++) {
+                const int h = h0 + ii;
+                const bool ok = tile_ok && c < a.C && h >= 0 && h < a.H;
+                const int o = a.xd + 2 * ((b * a.C + c) * HW + h * a.W + w0);
+                odd[j] |= (unsigned)((o >> 1) & 1) << ii;
+                neg[j] |= (ok && o < 0) ? (1u << ii) : 0u;
+                const int A = !ok ? kBOob : (o < 0 ? 0 : (o & ~3));
+                const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, A, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 4; q++) w5[j][ii][q] = v[q];
+                w5[j][ii][4] = __builtin_amdgcn_raw_buffer_load_b32(xrs, A + 16, 0, 0);
+            }
         }
     }
 
@@ -568,7 +612,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
     unsigned any_neg = 0;
 #pragma unroll
     for (int j = 0; j < NS; j++) any_neg |= neg[j];
-    if (__builtin_amdgcn_ballot_w64(any_neg != 0) != 0) {
+    if (!kNhwc && __builtin_amdgcn_ballot_w64(any_neg != 0) != 0) {
 #pragma unroll
         for (int j = 0; j < NS; j++) {
             const int c = ct + 32 * j;
@@ -601,9 +645,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
             const unsigned sb = ((odd[j] >> ii) & 1u) * 2;
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                d4[ii][q] = __builtin_amdgcn_alignbyte(w5[j][ii][q + 1], w5[j][ii][q], sb);
+                d4[ii][q] = kNhwc ? px[j][ii][q]
+                                  : __builtin_amdgcn_alignbyte(w5[j][ii][q + 1], w5[j][ii][q], sb);
         }
-        if (cmask != 0xffu) {
+        if (!kNhwc && cmask != 0xffu) {
 #pragma unroll
             for (int ii = 0; ii < 8; ii++)
 #pragma unroll
@@ -611,7 +656,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
         }
         if (j == 1) {
 #pragma unroll
-            for (int s = kPreU<NS>; s < kPreU<NS> + kMidU; s++) load_u(s);
+            for (int s = kPreU<NS>; s < kPreU<NS> + kMidU<kNhwc>; s++) load_u(s);
         }
         _Float16* vj = vs + j * 512;
         input_tile_rows(
@@ -644,12 +689,13 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                 acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[s][kb][1], vb[1],
                                                                     acc[s][kb], 0, 0, 0);
         }
-        constexpr int kAhead = kPreU<NS> + (NS == 2 ? kMidU : 0);  // positions already requested
+        constexpr int kAhead = kPreU<NS> + (NS == 2 ? kMidU<kNhwc> : 0);  // positions already requested
         if (s + kAhead < 8) load_u(s + kAhead);
     }
     __syncthreads();  // V becomes M
 
-    // ---- M (fp16) to LDS: [kk][tile][position], as the staged form ----
+    // ---- M (fp16) to LDS: [kk][tile][position] ([tile][kk][position] for
+    // channels-last), as the staged form ----
     _Float16* ms = reinterpret_cast<_Float16*>(lds);
     {
         const int g = lane >> 4, tq = lane & 15;
@@ -661,11 +707,15 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                 h8 v;
 #pragma unroll
                 for (int s = 0; s < 8; s++) v[s] = to_f16(acc[s][kb][i]);
-                *reinterpret_cast<h8*>(ms + (kk * 16 + tq) * kBMPitch + 8 * wave) = v;
+                const int mo = kNhwc ? tq * kNhwcTileP + kk * kBMPitch : (kk * 16 + tq) * kBMPitch;
+                *reinterpret_cast<h8*>(ms + mo + 8 * wave) = v;
             }
     }
     __syncthreads();
-    output_phase_nchw<kEpi>(a, ms, tid, t, tile_ok, th, tw, b, k0, yrs);
+    if constexpr (kNhwc)
+        output_phase_nhwc<kEpi>(a, ms, tid, ntiles, t0, b, k0, yrs);
+    else
+        output_phase_nchw<kEpi>(a, ms, tid, t, tile_ok, th, tw, b, k0, yrs);
 }
 
 int round16i(int v) { return (v + 15) & ~15; }
@@ -684,15 +734,16 @@ bool fused_block_plan(int B, int C, int K, int Cp, int H, int W, int nh, int nw,
     }
     const int rows_st = 6 * maxrows + 2;
     p->nhwc = nhwc;
-    if (nhwc) {
+    if (Cp <= 64) {
+        // the unstaged form (fused_block_kernel_direct): no limit on the image
+        // width, any C and any alignment of x
+        p->cols = p->rp = p->cp = p->nj = 0;
+    } else if (nhwc) {
         // [row][pixel][channel] staging; 16-byte channel groups need C % 8 == 0
         const int cols = 6 * nw + 2;
         if (C % 8 != 0 || rows_st * cols * kNhwcPix * 2 > kBXBytes) return false;
         p->cols = cols;
         p->rp = p->cp = p->nj = 0;
-    } else if (Cp <= 64) {
-        // the unstaged form (fused_block_kernel_direct): no limit on the image width
-        p->cols = p->rp = p->cp = p->nj = 0;
     } else {
         const int rp = round16i(2 * (6 * nw + 2) + 18);
         const int cp = rows_st * rp + 16;
@@ -753,16 +804,24 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
     const dim3 grid((unsigned)p.grid), block(kBT);
     const bool epi = epilogue_needed(ep.bias, ep.relu, ep.residual);
     auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
+    if (Cp <= 64) {
+        auto direct = [&](auto ns, auto nhwc) {
+            constexpr int NS = decltype(ns)::value;
+            constexpr bool kN = decltype(nhwc)::value;
+            epi ? go(fused_block_kernel_direct<NS, kN, true>)
+                : go(fused_block_kernel_direct<NS, kN, false>);
+        };
+        using one = std::integral_constant<int, 1>;
+        using two = std::integral_constant<int, 2>;
+        if (p.nhwc)
+            Cp > 32 ? direct(two(), std::true_type()) : direct(one(), std::true_type());
+        else
+            Cp > 32 ? direct(two(), std::false_type()) : direct(one(), std::false_type());
+        return hipGetLastError();
+    }
     if (p.nhwc) {
         if (a.xd != 0) return hipErrorInvalidValue;  // 16-byte loads need an aligned x
         epi ? go(fused_block_kernel<0, true, true>) : go(fused_block_kernel<0, true, false>);
-        return hipGetLastError();
-    }
-    if (Cp <= 64) {
-        if (Cp > 32)
-            epi ? go(fused_block_kernel_direct<2, true>) : go(fused_block_kernel_direct<2, false>);
-        else
-            epi ? go(fused_block_kernel_direct<1, true>) : go(fused_block_kernel_direct<1, false>);
         return hipGetLastError();
     }
     auto go_nj = [&](auto nj) {

@@ -1,5 +1,5 @@
-"""The unstaged NCHW form of the fused tile-block kernel (path 3 at up to 64
-input channels), through the C-ABI.
+"""The unstaged form of the fused tile-block kernel (path 3 at up to 64 input
+channels, NCHW and channels-last), through the C-ABI.
 
 Each thread loads its patch rows straight from global memory as a 16-byte
 and a 4-byte load from the dword at or below the row start, so the cases
@@ -9,8 +9,8 @@ the first row of the tensor (the rows that start before the buffer), images
 wider than the staged form allowed (nw > 10), one and two 32-channel steps,
 channel counts off the 8/16/32 blocks and more than one 64-channel output
 block. Every output is checked against the oracle; the same input at another
-alignment gives the same bits; where the staged channels-last form can run
-the same layer, it gives the same bits too (same transforms, same MFMA
+alignment gives the same bits, and so does the channels-last form from the
+same alignment (one 2-byte load per pixel; same transforms, same MFMA
 order).
 """
 
@@ -97,9 +97,12 @@ def test_fused_direct_matches_oracle(oracle, B, C, K, H, W, pad, off):
     # another alignment of the same input: the same bits
     y0, _ = _forward(lib, _at_offset(x.to(DEV), 0 if off else 5), wd, pad, 3)
     assert torch.equal(y0.cpu().view(torch.int16), yc.view(torch.int16))
-    # the staged channels-last form, where it runs: the same bits
-    if C % 8 == 0:
-        xc = x.to(DEV).contiguous(memory_format=torch.channels_last)
-        yn, took_n = _forward(lib, xc, wd, pad, 3, nhwc=True)
-        if took_n == 3:
-            assert torch.equal(yn.contiguous().cpu().view(torch.int16), yc.view(torch.int16))
+    # channels-last, from the same alignment: the same bits
+    n_el = x.numel()
+    store = torch.empty(n_el + 64, dtype=torch.float16, device=DEV)
+    xc = torch.as_strided(store, (B, C, H, W), (H * W * C, 1, W * C, C), storage_offset=off)
+    xc.copy_(x.to(DEV))
+    assert xc.is_contiguous(memory_format=torch.channels_last)
+    yn, took_n = _forward(lib, xc, wd, pad, 3, nhwc=True)
+    assert took_n == 3
+    assert torch.equal(yn.contiguous().cpu().view(torch.int16), yc.view(torch.int16))

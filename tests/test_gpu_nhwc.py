@@ -62,8 +62,8 @@ def test_nhwc_equals_nchw(B, C, K, H, pad):
     x = torch.randn(B, C, H, H, device=DEV).half()
     w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
     y, took = _run(x.contiguous(memory_format=CL), w, pad, True)
-    assert took in (1, 5, 6)  # three-pass, the small-problem kernel for small grids, or
-    #                            two-pass (conv3_x at batch 32, conv2_x at batch 8)
+    assert took in (1, 3, 5, 6)  # three-pass, fused tile-block, the small-problem kernel
+    #                               for small grids, or two-pass (conv3_x at batch 32)
     y_ref, took_ref = _run(x, w, pad, False, path=took)  # the same path in NCHW
     assert took_ref == took
     assert y.is_contiguous(memory_format=CL)
@@ -79,30 +79,20 @@ def test_nhwc_equals_nchw(B, C, K, H, pad):
 @pytest.mark.parametrize("B,C,K,H,pad", CASES + [(32, 64, 64, 56, 1), (2, 64, 64, 64, 1)])
 def test_nhwc_fused_block_equals_nchw(B, C, K, H, pad):
     """Forced tile-block fused path: NHWC equals NCHW bit for bit (same
-    transforms, same 16-channel MFMA steps), with and without the epilogue.
-    Out of the NHWC envelope (C % 8 != 0) it runs three-pass and reports it."""
-    from nova_winograd.ops import check
-
+    transforms, same 16-channel MFMA steps), with and without the epilogue,
+    at any channel count and image width (both layouts run the unstaged
+    form up to 64 input channels)."""
     print(f"[nhwc fused] B={B} C={C} K={K} H={H} pad={pad}", flush=True)
     torch.manual_seed(16)
     x = torch.randn(B, C, H, H, device=DEV).half()
     w = (torch.randn(K, C, 3, 3, device=DEV) * (2.0 / (9 * C)) ** 0.5).float()
     xc = x.contiguous(memory_format=CL)
-    if C % 8 != 0:
-        with pytest.raises(RuntimeError, match="fused path unsupported"):
-            _run(xc, w, pad, True, path=3)
-        check()
-        return
     y, took = _run(xc, w, pad, True, path=3)
     assert took == 3
     assert y.is_contiguous(memory_format=CL)
-    y_ref, took_ref = _run(x, w, pad, False, path=0 if H > 60 else 3)
-    if took_ref != 3:  # wider than the NCHW kernel's staging: compare with three-pass
-        a, b = y.float(), y_ref.float()
-        assert ((a - b).norm() / b.norm()).item() <= 2e-3
-        assert (a - b).abs().max().item() <= 0.1
-    else:
-        assert torch.equal(y, y_ref)
+    y_ref, took_ref = _run(x, w, pad, False, path=3)
+    assert took_ref == 3
+    assert torch.equal(y, y_ref)
     assert torch.isfinite(y).all()
     bias = (torch.randn(K, device=DEV) * 0.5).half()
     res = torch.randn_like(y).contiguous(memory_format=CL)
@@ -143,13 +133,12 @@ def test_nhwc_unaligned_input():
     assert x_cl.is_contiguous(memory_format=CL) and x_cl.data_ptr() % 16 != 0
     y, _ = _run(x_cl, w, 1, True)
     assert torch.equal(y, y_ref)
-    # the tile-block fused kernel stages with 16-byte loads: a forced fused
-    # path runs three-pass for this x and reports it
-    from nova_winograd.ops import check
-
-    with pytest.raises(RuntimeError, match="fused path unsupported"):
-        _run(x_cl, w, 1, True, path=3)
-    check()
+    # the unstaged fused tile-block form loads x 2 bytes at a time: it takes
+    # this x, and gives the NCHW form's bits
+    y3, took3 = _run(x_cl, w, 1, True, path=3)
+    assert took3 == 3
+    y3_ref, _ = _run(x, w, 1, False, path=3)
+    assert torch.equal(y3, y3_ref)
 
 
 def test_module_and_functional_channels_last():
