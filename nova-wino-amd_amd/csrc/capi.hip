@@ -403,14 +403,19 @@ int choose_path(const Handle* Hd, const Shape& s) {
     // B=64 29.3 vs 21.3; 32@56^2 B=8 18.7 vs 11.7, B=64 42.5 vs 23.3;
     // 64@112^2 B=8 33.4 vs 21.8, B=16 51.7 vs 41.5; 48->40@13^2 B=128 21.5
     // vs 19.5.
-    // Small problems (the small-problem kernel's grid at most two workgroups
-    // per CU): one launch of that kernel. Measured on MI355X, us, three-pass
-    // vs small kernel: conv2_x B=1 10.4 vs 7.5, B=2 12.0 vs 10.4 (B=4 16.9 vs
-    // 18.0: three-pass); 32@56^2 B=4 12.5 vs 9.7; 48->40@13^2 B=32 13.4 vs
-    // 10.2 (B=128 22.9 vs 31.0); 64@112^2 B=1 15.7 vs 16.1 (724 workgroups).
+    // Small problems: one launch of the small-problem kernel while its grid
+    // holds at most two workgroups per CU, four when the layer has two
+    // 32-channel chunks (with one, the fused tile-block kernel is cheaper
+    // there). Measured on MI355X, us, best other path vs small kernel:
+    // conv2_x B=1 10.4 vs 6.8 (three-pass), B=3 14.2 vs 12.3, B=4 15.2 vs
+    // 14.7 (two-pass), B=5 15.3 vs 15.5 (two-pass; 1000 workgroups);
+    // 64@112^2 B=1 14.9 vs 13.3; 48@112^2 B=1 14.1 vs 12.4; 48->40@13^2 B=64
+    // 15.1 vs 14.2; 32@56^2 B=4 11.0 vs 8.5, B=8 11.7 (fused tile-block) vs
+    // 13.6; 32@112^2 B=2 11.7 vs 12.2; beyond four per CU it loses (64@112^2
+    // B=2 16.2 vs 21.4; 48->40@13^2 B=128 16.9 vs 24.4).
     FusedSmallPlan sp;
     if (Hd->C <= 64 && Hd->K <= 64 && fused_small_plan_for(Hd, s, &sp) &&
-        sp.grid <= 2 * (int64_t)Hd->cus)
+        sp.grid <= (Hd->Cp > 32 ? 4 : 2) * (int64_t)Hd->cus)
         return 5;
     FusedBlockPlan bp;
     if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {

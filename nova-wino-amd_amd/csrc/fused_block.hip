@@ -91,6 +91,15 @@ __device__ __forceinline__ int v_index(int pos, int c, int t) {
     return (((pos * 4 + ((c >> 2) & 3)) * 16 + t) * 2 + ((c >> 4) & 1)) * 4 + (c & 3);
 }
 
+// v_index with the tile slot swizzled by the channel group (slot t ^ 4g for
+// group g = (c >> 2) & 3): the unstaged kernel's channels-last threads write
+// 32 channels of 2 tiles per instruction, whose 4 groups would otherwise
+// share banks (lanes over 16 tiles of one group, the NCHW threads, stay
+// conflict-free). Lane l reads its B operand at slot l ^ ((l >> 4) << 2).
+__device__ __forceinline__ int v_index_sw(int pos, int c, int t) {
+    return v_index(pos, c, t ^ (((c >> 2) & 3) << 2));
+}
+
 // Byte offset of the A operand of (position p, row tile kt, chunk j) in the
 // fragment-ordered U; out of range (reads zero) past the last row tile.
 __device__ __forceinline__ int u_off(const BlockArgs& a, int p, int kt, int j) {
@@ -667,7 +676,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                 return (float)__builtin_bit_cast(_Float16, bits);
             },
             [&](int r, int s2, float v) {
-                vj[(r * 8 + s2) * (NS * 512) + v_index(0, ct, t)] = to_f16(v);
+                vj[(r * 8 + s2) * (NS * 512) + v_index_sw(0, ct, t)] = to_f16(v);
             });
     }
     __syncthreads();
@@ -680,7 +689,8 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
         h8 vb[NS];
 #pragma unroll
         for (int j = 0; j < NS; j++)
-            vb[j] = *reinterpret_cast<const h8*>(vs + pos * (NS * 512) + j * 512 + lane * 8);
+            vb[j] = *reinterpret_cast<const h8*>(vs + pos * (NS * 512) + j * 512 +
+                                                 (lane ^ ((lane >> 4) << 2)) * 8);
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) {
             acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(

@@ -66,18 +66,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sm_rsrc(const void* p, int byt
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 
-// V in LDS, halves: [position][chunk][channel group of 4][tile slot][half of
-// the chunk][4 channels]: lane l's B operand (tile l % 16 < T, channels
-// 4*(l/16) .. +3 of both 16-channel halves) is 16 contiguous bytes.
-// Each position's block is padded by 8 halves (4 banks), so the 8 lanes of
-// a patch, which write 8 different positions, hit 8 different banks.
+// V in LDS, halves: [chunk][channel group of 4][tile slot][position slot]
+// [half of the chunk][4 channels], position slot (pos % 8) * 8 + pos / 8:
+// lane l's B operand (tile l % 16 < T, channels 4*(l/16) .. +3 of both
+// 16-channel halves) is 16 contiguous bytes. A transform write instruction
+// covers 8 position rows j (positions 8j + s) of 8 channels: with the
+// position slots in that order its 8 j's land 4 dwords apart, and the
+// (chunk, group, tile) blocks of sm_blk_halves put its two channel groups 32
+// banks apart, so the 64 lanes hit 32 banks, one dword each (the earlier
+// [position][...] order, 8 positions 544 dwords apart, put them in 8 banks).
+constexpr int sm_blk_halves() { return 64 * 8 + 32; }  // T = 2: groups 32 banks apart
 template <int T, int NKP>
-constexpr int sm_pos_halves() {
-    return NKP * 4 * T * 8 + 8;
+constexpr int sm_v_halves() {
+    return NKP * 4 * T * sm_blk_halves();
 }
 template <int T, int NKP>
 __device__ __forceinline__ int sm_v_base(int pos, int chunk, int cg, int t) {
-    return pos * sm_pos_halves<T, NKP>() + ((chunk * 4 + cg) * T + t) * 8;
+    return ((chunk * 4 + cg) * T + t) * sm_blk_halves() + ((pos & 7) * 8 + (pos >> 3)) * 8;
 }
 template <int T, int NKP>
 __device__ __forceinline__ int sm_v_index(int pos, int c, int t) {
@@ -97,7 +102,7 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     constexpr int kPpr = NTH / 8;                              // patches per round
     static_assert(kPatches % kPpr == 0, "whole rounds");
     constexpr int kRounds = kPatches / kPpr;
-    constexpr int kVHalves = 64 * sm_pos_halves<T, NKP>();     // V of the group's tiles
+    constexpr int kVHalves = sm_v_halves<T, NKP>();            // V of the group's tiles
     constexpr int kTpFloats = kPpr * kSmPitch;                 // one transpose buffer
     __shared__ __align__(16) _Float16 vs[kVHalves + 8];        // + one zero block
     __shared__ __align__(16) float tps[2][kTpFloats];          // double-buffered transposes

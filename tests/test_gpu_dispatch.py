@@ -82,7 +82,10 @@ AUTO_CASES = [
     (32, 128, 512, 7, 1),   # more than 256 output channels: three-pass
     (1, 64, 64, 56, 5),    # B=1: the small-problem kernel (200 workgroups)
     (2, 64, 64, 56, 5),    # 400 workgroups
-    (4, 64, 64, 56, 1),    # 800 workgroups: three-pass
+    (3, 64, 64, 56, 5),    # 600 workgroups, two 32-channel chunks: 12.3 vs 14.2 us
+    (4, 64, 64, 56, 5),    # 800 workgroups: 14.7 vs 15.2 us (two-pass)
+    (1, 64, 64, 112, 5),   # 724 workgroups: 13.3 vs 14.9 us
+    (2, 64, 64, 112, 6),   # 1448 workgroups: small kernel 21.4 vs two-pass 16.2 us
     (32, 48, 40, 13, 5),   # small images: 480 workgroups
 ]
 
