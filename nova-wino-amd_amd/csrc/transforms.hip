@@ -201,14 +201,18 @@ struct InGeom {
                                                                    // alignment slack, one dword
                                                                    // of read-ahead)
     static constexpr int kNJ = kRP / 16;                           // loads per span
-    // Channel pitch 8 x odd: lanes over consecutive channels then hit at most
-    // two channels per LDS bank (staging writes are 8-byte halves).
-    static constexpr int kCP = 8 * kRP + 8;
+    // Channel pitch: an odd number of dwords for TW = 2 and 4, so the compute
+    // threads (lanes over 64-128 consecutive channels, one dword per read)
+    // spread over all 64 banks: rocprofv3 SQ_LDS_BANK_CONFLICT at ResNet-50
+    // conv4_x batch 32 (TW = 4) read 2.6x the LDS's active cycles with an
+    // even pitch; staging writes are then single dwords. For TW = 8 an odd
+    // multiple of 8 bytes conflicts less (2-way at most on the reads).
+    static constexpr int kCP = TW == 8 ? 8 * kRP + 8 : 8 * kRP + 4;
     static constexpr int kUnits = kCB * 8 / 256;                    // (channel, row) spans per
                                                                    // thread
     static constexpr int kBytes = kCB * kCP;
     static_assert(kCB * 8 % 256 == 0, "staged spans must tile the workgroup");
-    static_assert((kCP / 8) % 2 == 1, "channel pitch must be an odd number of 8-byte units");
+    static_assert(TW == 8 ? (kCP / 8) % 2 == 1 : (kCP / 4) % 2 == 1, "odd channel pitch");
     __device__ static int base(int c) { return c * kCP; }
 };
 
@@ -247,8 +251,13 @@ __device__ __forceinline__ void input_stage(unsigned char* sx, __amdgpu_buffer_r
 #pragma unroll
         for (int q = 0; q < G::kNJ; q++) {
             unsigned char* d = dst + 32 * u * G::kCP + 16 * q;
-            *reinterpret_cast<u2*>(d) = u2{val[u][q][0], val[u][q][1]};
-            *reinterpret_cast<u2*>(d + 8) = u2{val[u][q][2], val[u][q][3]};
+            if constexpr (G::kCP % 8 == 0) {
+                *reinterpret_cast<u2*>(d) = u2{val[u][q][0], val[u][q][1]};
+                *reinterpret_cast<u2*>(d + 8) = u2{val[u][q][2], val[u][q][3]};
+            } else {  // 4-byte aligned spans
+#pragma unroll
+                for (int k = 0; k < 4; k++) reinterpret_cast<unsigned*>(d)[k] = val[u][q][k];
+            }
         }
 }
 
@@ -608,8 +617,11 @@ template <int TW>
 struct OutGeom {
     static constexpr int kKB = 256 / TW;          // output channels per workgroup
     static constexpr int kCols = TW * 6;          // output columns per block
-    static constexpr int kPlane = 6 * kCols + 4;  // halves per channel: 8-byte rows,
-                                                  // at most 2-way write conflicts
+    // halves per channel: with 8-byte segments (kVW = 4) a multiple of 4
+    // (2-way write conflicts, lanes over consecutive channels); otherwise an
+    // odd number of dwords, so the 64 lanes of a write hit 64 banks
+    template <int kVW>
+    static constexpr int plane() { return kVW == 4 ? 6 * kCols + 4 : 6 * kCols + 2; }
 };
 
 template <int TW, int kVW, bool kEpi>
@@ -618,7 +630,8 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
     const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
     using G = OutGeom<TW>;
-    __shared__ __align__(16) _Float16 sy[G::kKB * G::kPlane];
+    constexpr int kPlane = G::template plane<kVW>();
+    __shared__ __align__(16) _Float16 sy[G::kKB * kPlane];
     const int nwb = (nw + TW - 1) / TW;
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int tw0 = (L % nwb) * TW;
@@ -646,7 +659,7 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
         float out[6][6];
         output_tile([&](int i, int j) { return (float)__builtin_bit_cast(_Float16, m[i * 8 + j]); },
                     out);
-        _Float16* sp = sy + kk * G::kPlane + t * 6;
+        _Float16* sp = sy + kk * kPlane + t * 6;
         const ChannelEpilogue<kEpi> epi(bias, k, res ? 0 : relu);
 #pragma unroll
         for (int r = 0; r < 6; r++)
@@ -675,7 +688,7 @@ __global__ __launch_bounds__(256) void output_transform_kernel(
     // residual (same layout as y): added per stored segment, then the ReLU
     const __amdgpu_buffer_rsrc_t rrs = make_rsrc(res, res ? y_bytes : 0);
     for (; e < total; e += 256) {
-        const _Float16* src = sy + kk * G::kPlane + r * G::kCols + sg * kVW;
+        const _Float16* src = sy + kk * kPlane + r * G::kCols + sg * kVW;
         const int off = ybase + 2 * ((kk * Ho + r) * Wo + sg * kVW);
         if (sg * kVW + kVW <= ncols) {
             if constexpr (kVW == 4) {
