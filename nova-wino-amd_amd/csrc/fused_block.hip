@@ -498,14 +498,14 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 // shifted into place in a branch that only the wave holding them takes.
 // ---------------------------------------------------------------------------
 // Positions whose U operands are requested before the transform (one step:
-// 6; two steps: 3, and kMidU more once the first patch is transformed: 3,
-// or 2 channels-last, whose packed patch pairs leave fewer registers).
+// 6; two steps: 3, and kMidU = 2 more once the first patch is transformed,
+// as many as fit beside the transform's registers without spilling).
 // Whole forwards, graph of ten, us: conv2_x B=32 22.25 (3 before) -> 21.43
 // (3 + 3), B=128 78.7 -> 76.5; C = 32 B=32 12.75 (3) -> 12.49 (6).
 template <int NS>
 constexpr int kPreU = NS == 1 ? 6 : 3;
 template <bool kNhwc>
-constexpr int kMidU = kNhwc ? 2 : 3;
+constexpr int kMidU = 2;
 
 template <int NS, bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a) {
@@ -668,6 +668,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
             for (int s = kPreU<NS>; s < kPreU<NS> + kMidU<kNhwc>; s++) load_u(s);
         }
         _Float16* vj = vs + j * 512;
+        float pend = 0.0f;  // NCHW: the even position of the pair being written
         input_tile_rows(
             [&](int ii, int jj) {
                 const unsigned pr = d4[ii][jj >> 1];
@@ -676,7 +677,29 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                 return (float)__builtin_bit_cast(_Float16, bits);
             },
             [&](int r, int s2, float v) {
-                vj[(r * 8 + s2) * (NS * 512) + v_index_sw(0, ct, t)] = to_f16(v);
+                if constexpr (kNhwc) {
+                    vj[(r * 8 + s2) * (NS * 512) + v_index_sw(0, ct, t)] = to_f16(v);
+                } else {
+                    // Channels c and c ^ 1 share a dword of V and sit 16 lanes
+                    // apart (lane row = c % 4). Per pair of positions (p, p + 1)
+                    // one row swap gives the even row both channels at p and
+                    // the odd row both at p + 1: one 4-byte write per lane
+                    // instead of two 2-byte writes into shared dwords.
+                    if ((s2 & 1) == 0) {
+                        pend = v;
+                        return;
+                    }
+                    const auto sw = __builtin_amdgcn_permlane16_swap(
+                        __builtin_bit_cast(unsigned, pend), __builtin_bit_cast(unsigned, v), false,
+                        false);
+                    const unsigned lo = __builtin_bit_cast(
+                        uint16_t, to_f16(__builtin_bit_cast(float, (unsigned)sw[0])));
+                    const unsigned hi = __builtin_bit_cast(
+                        uint16_t, to_f16(__builtin_bit_cast(float, (unsigned)sw[1])));
+                    const int pos = r * 8 + s2 - 1 + (ct & 1);
+                    *reinterpret_cast<unsigned*>(vj + pos * (NS * 512) +
+                                                 v_index_sw(0, ct & ~1, t)) = lo | (hi << 16);
+                }
             });
     }
     __syncthreads();
