@@ -491,6 +491,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 //   * each wave then finishes one position at a time (both steps, the first
 //     MFMA from a zero accumulator), requesting the next position's
 //     operands as registers free up;
+//   * V is written in the staged form's operand layout with the tile slots
+//     swizzled by channel group (v_index_sw); NCHW pairs channels c, c ^ 1
+//     across lane rows with one v_permlane16_swap per two positions, so
+//     every lane writes whole dwords;
 //   * after a barrier, M is written over V (as the staged form lays it out
 //     for the layout) and the output phase is the staged form's.
 // Rows that start before x_al (only the first row of channel 0 of image 0
@@ -501,10 +505,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
 // 6; two steps: 3, and kMidU = 2 more once the first patch is transformed,
 // as many as fit beside the transform's registers without spilling).
 // Whole forwards, graph of ten, us: conv2_x B=32 22.25 (3 before) -> 21.43
-// (3 + 3), B=128 78.7 -> 76.5; C = 32 B=32 12.75 (3) -> 12.49 (6).
+// (3 + 3, before the paired V writes, which leave room for 2); C = 32 B=32
+// 12.75 (3) -> 12.49 (6).
 template <int NS>
 constexpr int kPreU = NS == 1 ? 6 : 3;
-template <bool kNhwc>
 constexpr int kMidU = 2;
 
 template <int NS, bool kNhwc, bool kEpi>
@@ -665,7 +669,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
         }
         if (j == 1) {
 #pragma unroll
-            for (int s = kPreU<NS>; s < kPreU<NS> + kMidU<kNhwc>; s++) load_u(s);
+            for (int s = kPreU<NS>; s < kPreU<NS> + kMidU; s++) load_u(s);
         }
         _Float16* vj = vs + j * 512;
         float pend = 0.0f;  // NCHW: the even position of the pair being written
@@ -722,7 +726,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                 acc[s][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ua[s][kb][1], vb[1],
                                                                     acc[s][kb], 0, 0, 0);
         }
-        constexpr int kAhead = kPreU<NS> + (NS == 2 ? kMidU<kNhwc> : 0);  // positions already requested
+        constexpr int kAhead = kPreU<NS> + (NS == 2 ? kMidU : 0);  // positions already requested
         if (s + kAhead < 8) load_u(s + kAhead);
     }
     __syncthreads();  // V becomes M
