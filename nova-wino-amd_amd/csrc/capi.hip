@@ -335,6 +335,33 @@ bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
     return fused_small_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, p);
 }
 
+// First tile of the short last 16-tile run of every image when the tile-block
+// kernel should leave those tiles to the small-problem kernel (0: it takes
+// every tile). A short run costs a workgroup as much as a full one; where
+// the full runs alone need one round of workgroups less (one workgroup per
+// CU), the short runs' tiles go to a second launch of the small-problem
+// kernel (2 tiles x 16 output channels per workgroup, spread over every CU),
+// while that launch has at most 2 workgroups per CU (1 at one 32-channel
+// chunk): a round of the tile-block kernel costs ~19 us at two chunks, the
+// small-problem launch ~11 us at 1.25 workgroups per CU, ~17 at 2.5 and ~21
+// at 4. Whole forwards, graph of ten, us, one launch vs split: 64@56^2
+// batch 37 36.9 vs 31.3, 40 36.9 vs 32.2, 42 39.8 vs 32.5, 80 56.1 vs 55.6,
+// 128 78.2 vs 79.5 (not split); 64@54^2 pad 2 batch 43 (81 tiles) 39.6 vs
+// 29.6; 32@56^2 batch 40 21.4 vs 18.9. Both kernels give the same bits for
+// a tile.
+int fused_tail_first(const Handle* Hd, const Shape& s, const FusedBlockPlan& bp) {
+    const int P = s.nh * s.nw, full = P / 16;
+    if (full == 0 || P % 16 == 0 || Hd->C > 64 || Hd->K > 64 || Hd->Cp > 64) return 0;
+    const int64_t cus = Hd->cus;
+    const int64_t g_full = (int64_t)s.B * full * bp.n_kblk;
+    if ((g_full + cus - 1) / cus >= (bp.grid + cus - 1) / cus) return 0;
+    FusedSmallPlan sp;
+    if (!fused_small_plan(s.B, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, &sp, 16 * full) ||
+        sp.grid > (Hd->Cp > 32 ? 2 : 1) * cus)
+        return 0;
+    return 16 * full;
+}
+
 // Layers the automatic choice may send to the two-pass path (their handles
 // build the two-pass copy of U with the weights).
 bool two_pass_possible(int C, int K) { return C <= 128 && K <= 256 && 2 * K >= C; }
@@ -421,7 +448,20 @@ int choose_path(const Handle* Hd, const Shape& s) {
     if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
         const int chunks = (Hd->Cp + 31) / 32;
-        const double t_fused = 3.0 + (double)waves * 9.2 * chunks;
+        double t_fused = 3.0 + (double)waves * 9.2 * chunks;
+        // with the short runs split off (fused_tail_first): the full runs'
+        // rounds plus the small-problem launch (~6 us + 4 us per workgroup
+        // per CU: 11 us at 1.25, measured at 64@56^2 batch 40)
+        Shape sb = s;
+        sb.B = (int)sub_batch(Hd, s);
+        const int tail = fused_tail_first(Hd, sb, bp);
+        FusedSmallPlan tp;
+        if (tail > 0 && fused_small_plan(sb.B, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, &tp,
+                                         tail)) {
+            const int64_t g_full = (int64_t)sb.B * (tail / 16) * bp.n_kblk;
+            t_fused = 3.0 + (double)((g_full + Hd->cus - 1) / Hd->cus) * 9.2 * chunks + 6.0 +
+                      4.0 * (double)tp.grid / Hd->cus;
+        }
         const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
                            4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
         const double t_three = 10.0 + s.B * img / 5.0e6;  // bytes / (5 TB/s) in us
@@ -706,9 +746,23 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                 set_error(kErrInvalidArgument, "%s: no fused plan for this sub-batch", fn);
                 return;
             }
+            // the short last run of every image to the small-problem kernel
+            // when that saves the tile-block kernel a round of workgroups
+            const int tail = fused_tail_first(Hd, s, bp);
+            FusedSmallPlan sp{};
+            if (tail > 0) {
+                bp.nruns = tail / 16;
+                bp.grid = (int64_t)s.B * bp.nruns * bp.n_kblk;
+                fused_small_plan((int)s.B, C, K, Cp, s.nh, s.nw, Hd->cus, &sp, tail);
+            }
+            const bool nhwc = Hd->nhwc != 0;
             auto fz = [=]() {
-                return launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
-                                          s.Ho, s.Wo, bp, st, ep);
+                hipError_t e = launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad,
+                                                  s.nh, s.nw, s.Ho, s.Wo, bp, st, ep);
+                if (e == hipSuccess && tail > 0)
+                    e = launch_fused_small(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
+                                           s.Ho, s.Wo, sp, st, ep, nhwc);
+                return e;
             };
             if (b0 == 0 && !no_alloc) {
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;

@@ -53,7 +53,8 @@ struct SmallArgs {
     _Float16* y;
     int x_bytes, u_bytes, y_bytes;
     int C, K, H, W, pad, nh, nw, Ho, Wo, P;
-    int ntg;       // tile groups per image
+    int tfirst;    // first tile of each image
+    int ntg;       // tile groups per image, from tfirst on
     int nkb;       // 16-channel output blocks
     int nkt, nkp;  // 16-row tiles and 32-channel chunks of the fragment-ordered U
     int y_pairs;   // 1: NCHW rows stored as 4-byte pairs (even Wo, 4-byte aligned y)
@@ -116,7 +117,7 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     const int tg = rest % a.ntg;
     const int b = rest / a.ntg;
     const int k0 = kb * kSmK;
-    const int t0 = tg * T;
+    const int t0 = a.tfirst + tg * T;
     const int ntiles = min(T, a.P - t0);
 
     const __amdgpu_buffer_rsrc_t xrs = sm_rsrc(a.x, a.x_bytes);
@@ -317,15 +318,18 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
 
 }  // namespace
 
-bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus, FusedSmallPlan* p) {
+bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus, FusedSmallPlan* p,
+                      int tfirst) {
     if (B < 1 || C < 1 || K < 1 || C > 128 || K > 128 || Cp > 128) return false;
+    if (tfirst < 0 || tfirst >= nh * nw) return false;
     p->nkp = Cp <= 64 ? 2 : 4;
     const int P = nh * nw;
     // 2 tiles per workgroup: measured at conv2_x batch 1 (100 tiles), one
     // launch of 1, 2 or 4 tiles per workgroup took 8.3, 7.4 and 9.4 us (the
     // input transform of a workgroup's tiles runs on one CU)
     p->tiles = 2;
-    p->ntg = (P + p->tiles - 1) / p->tiles;
+    p->tfirst = tfirst;
+    p->ntg = (P - tfirst + p->tiles - 1) / p->tiles;
     p->nkb = (K + kSmK - 1) / kSmK;
     p->grid = (int64_t)B * p->ntg * p->nkb;
     // 1024 threads (one transform round, 4 positions per wave) while every
@@ -360,6 +364,7 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.Ho = Ho;
     a.Wo = Wo;
     a.P = nh * nw;
+    a.tfirst = p.tfirst;
     a.ntg = p.ntg;
     a.nkb = p.nkb;
     a.nkt = (K + 15) / 16;

@@ -179,14 +179,15 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
 // fill the chip (batch 1).
 struct FusedSmallPlan {
     int tiles;  // tiles per workgroup
-    int ntg;    // tile groups per image
+    int tfirst; // first tile of each image (tiles before it are left to another launch)
+    int ntg;    // tile groups per image, from tfirst on
     int nkb;    // 16-channel output blocks
     int threads;  // workgroup size: 512 or 1024
     int nkp;      // 32-channel input chunks held in LDS: 2 (C <= 64) or 4 (C <= 128)
     int64_t grid;
 };
 bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus,
-                      FusedSmallPlan* p);
+                      FusedSmallPlan* p, int tfirst = 0);
 hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
                               int Wo, const FusedSmallPlan& p, hipStream_t s,

@@ -64,6 +64,9 @@ AUTO_CASES = [
     (48, 64, 64, 56, 3),   # two waves, 46 vs 49 us (measured 50.5 vs 49.1: a near miss)
     (64, 64, 64, 56, 3),   # two waves, 46 vs 62 us
     (128, 64, 64, 56, 3),  # four waves
+    (40, 64, 64, 56, 3),   # 280 workgroups: the 240 full runs fill one round, the
+                           # short ones go to the small kernel, 32.2 vs 37.1 us
+    (37, 48, 64, 56, 3),   # the same split: 40.0 us three-pass before it was modelled
     (16, 64, 64, 56, 6),   # two-pass (200 workgroups, one round) 20.0 vs tile-block 23.6 us
     (48, 64, 64, 28, 6),   # two-pass 19.2 vs tile-block 23.1 us
     (80, 64, 64, 28, 3),   # 250 workgroups: tile-block 23.8 vs two-pass 25.1 us
