@@ -340,26 +340,32 @@ bool fused_small_plan_for(const Handle* Hd, const Shape& s, FusedSmallPlan* p) {
 // every tile). A short run costs a workgroup as much as a full one; where
 // the full runs alone need one round of workgroups less (one workgroup per
 // CU), the short runs' tiles go to a second launch of the small-problem
-// kernel (2 tiles x 16 output channels per workgroup, spread over every CU),
-// while that launch has at most 2 workgroups per CU (1 at one 32-channel
-// chunk): a round of the tile-block kernel costs ~19 us at two chunks, the
-// small-problem launch ~11 us at 1.25 workgroups per CU, ~17 at 2.5 and ~21
-// at 4. Whole forwards, graph of ten, us, one launch vs split: 64@56^2
-// batch 37 36.9 vs 31.3, 40 36.9 vs 32.2, 42 39.8 vs 32.5, 80 56.1 vs 55.6,
-// 128 78.2 vs 79.5 (not split); 64@54^2 pad 2 batch 43 (81 tiles) 39.6 vs
-// 29.6; 32@56^2 batch 40 21.4 vs 18.9. Both kernels give the same bits for
-// a tile.
-int fused_tail_first(const Handle* Hd, const Shape& s, const FusedBlockPlan& bp) {
+// kernel (2 tiles x 16 output channels per workgroup, else 4 tiles, spread
+// over every CU), while that launch has at most 2 workgroups per CU (1 at
+// one 32-channel chunk): a round of the tile-block kernel costs ~19 us at
+// two chunks, the small-problem launch of 2-tile workgroups ~11 us at 1.25
+// per CU, ~17 at 2.5 and ~21 at 4, of 4-tile ones ~18 at 2. Whole forwards,
+// graph of ten, us, one launch vs split: 64@56^2 batch 37 36.9 vs 31.3, 40
+// 36.9 vs 32.2, 42 39.8 vs 32.5 (2 tiles); 74 55.8 vs 54.0, 80 56.1 vs 55.4
+// (55.6 with 2 tiles), 85 59.4 vs 56.5, 112 74.6 vs 74.1, 128 78.4 vs 76.9
+// (79.5 with 2 tiles), channels-last 78.3 vs 76.5 (4 tiles); 64@54^2 pad 2
+// batch 43 (81 tiles) 39.6 vs 29.6; 32@56^2 batch 40 21.4 vs 18.9. Both
+// kernels give the same bits for a tile.
+int fused_tail_first(const Handle* Hd, const Shape& s, const FusedBlockPlan& bp,
+                     FusedSmallPlan* tp) {
     const int P = s.nh * s.nw, full = P / 16;
     if (full == 0 || P % 16 == 0 || Hd->C > 64 || Hd->K > 64 || Hd->Cp > 64) return 0;
     const int64_t cus = Hd->cus;
     const int64_t g_full = (int64_t)s.B * full * bp.n_kblk;
     if ((g_full + cus - 1) / cus >= (bp.grid + cus - 1) / cus) return 0;
-    FusedSmallPlan sp;
-    if (!fused_small_plan(s.B, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, &sp, 16 * full) ||
-        sp.grid > (Hd->Cp > 32 ? 2 : 1) * cus)
-        return 0;
-    return 16 * full;
+    const int64_t limit = (Hd->Cp > 32 ? 2 : 1) * cus;
+    // 2 tiles per small-problem workgroup, else 4 (half the workgroups)
+    for (int tiles : {2, 4})
+        if (fused_small_plan(s.B, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, tp, 16 * full,
+                             tiles) &&
+            tp->grid <= limit)
+            return 16 * full;
+    return 0;
 }
 
 // Layers the automatic choice may send to the two-pass path (their handles
@@ -450,17 +456,16 @@ int choose_path(const Handle* Hd, const Shape& s) {
         const int chunks = (Hd->Cp + 31) / 32;
         double t_fused = 3.0 + (double)waves * 9.2 * chunks;
         // with the short runs split off (fused_tail_first): the full runs'
-        // rounds plus the small-problem launch (~6 us + 4 us per workgroup
-        // per CU: 11 us at 1.25, measured at 64@56^2 batch 40)
+        // rounds plus the small-problem launch (~6 us + 4 us per 2-tile
+        // workgroup per CU: 11 us at 1.25, measured at 64@56^2 batch 40)
         Shape sb = s;
         sb.B = (int)sub_batch(Hd, s);
-        const int tail = fused_tail_first(Hd, sb, bp);
         FusedSmallPlan tp;
-        if (tail > 0 && fused_small_plan(sb.B, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, Hd->cus, &tp,
-                                         tail)) {
+        const int tail = fused_tail_first(Hd, sb, bp, &tp);
+        if (tail > 0) {
             const int64_t g_full = (int64_t)sb.B * (tail / 16) * bp.n_kblk;
             t_fused = 3.0 + (double)((g_full + Hd->cus - 1) / Hd->cus) * 9.2 * chunks + 6.0 +
-                      4.0 * (double)tp.grid / Hd->cus;
+                      2.0 * tp.tiles * (double)tp.grid / Hd->cus;
         }
         const double img = 2.0 * Hd->C * s.H * s.W + 2.0 * Hd->K * s.Ho * s.Wo +
                            4.0 * 64 * (Hd->Cp + Hd->K) * (double)s.nh * s.nw;
@@ -748,12 +753,11 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             }
             // the short last run of every image to the small-problem kernel
             // when that saves the tile-block kernel a round of workgroups
-            const int tail = fused_tail_first(Hd, s, bp);
             FusedSmallPlan sp{};
+            const int tail = fused_tail_first(Hd, s, bp, &sp);
             if (tail > 0) {
                 bp.nruns = tail / 16;
                 bp.grid = (int64_t)s.B * bp.nruns * bp.n_kblk;
-                fused_small_plan((int)s.B, C, K, Cp, s.nh, s.nw, Hd->cus, &sp, tail);
             }
             const bool nhwc = Hd->nhwc != 0;
             auto fz = [=]() {

@@ -319,15 +319,18 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
 }  // namespace
 
 bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus, FusedSmallPlan* p,
-                      int tfirst) {
+                      int tfirst, int tiles) {
     if (B < 1 || C < 1 || K < 1 || C > 128 || K > 128 || Cp > 128) return false;
     if (tfirst < 0 || tfirst >= nh * nw) return false;
     p->nkp = Cp <= 64 ? 2 : 4;
+    if (tiles != 2 && (tiles != 4 || p->nkp != 2)) return false;
     const int P = nh * nw;
     // 2 tiles per workgroup: measured at conv2_x batch 1 (100 tiles), one
     // launch of 1, 2 or 4 tiles per workgroup took 8.3, 7.4 and 9.4 us (the
-    // input transform of a workgroup's tiles runs on one CU)
-    p->tiles = 2;
+    // input transform of a workgroup's tiles runs on one CU); 4 on request
+    // (up to 64 input channels), for grids that would otherwise hold more
+    // than two workgroups per CU
+    p->tiles = tiles;
     p->tfirst = tfirst;
     p->ntg = (P - tfirst + p->tiles - 1) / p->tiles;
     p->nkb = (K + kSmK - 1) / kSmK;
@@ -378,25 +381,32 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.relu = ep.relu;
     a.residual = reinterpret_cast<const _Float16*>(ep.residual);
     const dim3 grid((unsigned)p.grid), block((unsigned)p.threads);
-    if (p.tiles != 2 || (p.threads != 512 && p.threads != 1024) ||
+    if ((p.tiles != 2 && (p.tiles != 4 || p.nkp != 2)) || (p.threads != 512 && p.threads != 1024) ||
         (p.nkp != 2 && p.nkp != 4) || (p.nkp == 4 && p.threads != 1024) || Cp > 32 * p.nkp)
         return hipErrorInvalidConfiguration;
     auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
-    auto go_th = [&](auto nth, auto nkp) {
-        constexpr int N = decltype(nth)::value, NK = decltype(nkp)::value;
+    auto go_th = [&](auto tl, auto nth, auto nkp) {
+        constexpr int T = decltype(tl)::value, N = decltype(nth)::value,
+                      NK = decltype(nkp)::value;
         if (epilogue_needed(ep.bias, ep.relu, ep.residual))
-            nhwc ? go(fused_small_kernel<2, N, NK, true, true>)
-                 : go(fused_small_kernel<2, N, NK, false, true>);
+            nhwc ? go(fused_small_kernel<T, N, NK, true, true>)
+                 : go(fused_small_kernel<T, N, NK, false, true>);
         else
-            nhwc ? go(fused_small_kernel<2, N, NK, true, false>)
-                 : go(fused_small_kernel<2, N, NK, false, false>);
+            nhwc ? go(fused_small_kernel<T, N, NK, true, false>)
+                 : go(fused_small_kernel<T, N, NK, false, false>);
     };
+    using two = std::integral_constant<int, 2>;
+    using four = std::integral_constant<int, 4>;
+    using n1024 = std::integral_constant<int, 1024>;
+    using n512 = std::integral_constant<int, 512>;
     if (p.nkp == 4)
-        go_th(std::integral_constant<int, 1024>(), std::integral_constant<int, 4>());
+        go_th(two(), n1024(), four());
+    else if (p.tiles == 4)
+        p.threads == 1024 ? go_th(four(), n1024(), two()) : go_th(four(), n512(), two());
     else if (p.threads == 1024)
-        go_th(std::integral_constant<int, 1024>(), std::integral_constant<int, 2>());
+        go_th(two(), n1024(), two());
     else
-        go_th(std::integral_constant<int, 512>(), std::integral_constant<int, 2>());
+        go_th(two(), n512(), two());
     return hipGetLastError();
 }
 

@@ -187,7 +187,7 @@ struct FusedSmallPlan {
     int64_t grid;
 };
 bool fused_small_plan(int B, int C, int K, int Cp, int nh, int nw, int cus,
-                      FusedSmallPlan* p, int tfirst = 0);
+                      FusedSmallPlan* p, int tfirst = 0, int tiles = 2);
 hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y, int B, int C,
                               int K, int Cp, int H, int W, int pad, int nh, int nw, int Ho,
                               int Wo, const FusedSmallPlan& p, hipStream_t s,

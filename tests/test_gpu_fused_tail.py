@@ -3,9 +3,9 @@ the small-problem kernel (path 3 at batches where the full 16-tile runs need
 one round of workgroups less than all runs), through the C-ABI.
 
 At ResNet-50 conv2_x (100 tiles per image: six full runs and one of 4
-tiles) the split happens at batches 37-42 on 256 CUs (at 74-85 and 110-128
-the full runs would also save a round, but the small-problem launch would
-hold more than 2 workgroups per CU, where it costs more than the round). A tile
+tiles) the split happens at batches 37-42 on 256 CUs with 2 tiles per
+small-problem workgroup, and at 74-85 and 110-128 with 4 (2 would put more
+than 2 workgroups on a CU). A tile
 gives the same bits in either kernel, and every image is independent, so
 the batch is checked bit for bit against the same images run in batches of
 eight (where no split happens), NCHW and channels-last, with and without a
@@ -46,11 +46,11 @@ def _forward(lib, x, w, pad, nhwc=False, bias=None, relu=0):
     return y
 
 
-# (B, C, K, H, pad); on 256 CUs every case but batch 128 splits
+# (B, C, K, H, pad); on 256 CUs every case splits
 CASES = [
     (40, 64, 64, 56, 1),    # conv2_x: 280 workgroups, 240 full runs
     (37, 48, 64, 56, 1),    # 259 workgroups, 222 full runs, 48 input channels
-    (128, 64, 64, 56, 1),   # conv2_x: 896 workgroups; not split (tail launch too wide)
+    (128, 64, 64, 56, 1),   # conv2_x: 896 workgroups, 768 full runs, 4-tile tail groups
     (40, 40, 24, 56, 1),    # channel counts off the 32/16 blocks
     (40, 32, 32, 56, 1),    # one 32-channel chunk
     (43, 64, 64, 52, 2),    # 81 tiles per image: a 1-tile last run
