@@ -457,7 +457,8 @@ int choose_path(const Handle* Hd, const Shape& s) {
         double t_fused = 3.0 + (double)waves * 9.2 * chunks;
         // with the short runs split off (fused_tail_first): the full runs'
         // rounds plus the small-problem launch (~6 us + 4 us per 2-tile
-        // workgroup per CU: 11 us at 1.25, measured at 64@56^2 batch 40)
+        // workgroup per CU, a 4-tile one counted twice: 11 us at 1.25 2-tile
+        // workgroups per CU at 64@56^2 batch 40)
         Shape sb = s;
         sb.B = (int)sub_batch(Hd, s);
         FusedSmallPlan tp;
