@@ -5,11 +5,11 @@ one round of workgroups less than all runs), through the C-ABI.
 At ResNet-50 conv2_x (100 tiles per image: six full runs and one of 4
 tiles) the split happens at batches 37-42 on 256 CUs with 2 tiles per
 small-problem workgroup, and at 74-85 and 110-128 with 4 (2 would put more
-than 2 workgroups on a CU). A tile
-gives the same bits in either kernel, and every image is independent, so
-the batch is checked bit for bit against the same images run in batches of
-eight (where no split happens), NCHW and channels-last, with and without a
-bias/ReLU epilogue, and its first two images against the oracle.
+than 2 workgroups on a CU). A tile gives the same bits in either kernel,
+and every image is independent, so the batch is checked bit for bit
+against the same images run in batches of eight (where no split happens),
+NCHW and channels-last, with and without a bias/ReLU epilogue, and its
+first two images against the oracle.
 """
 
 import pytest
