@@ -18,7 +18,7 @@ import ctypes
 import math
 import threading
 import weakref
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -365,6 +365,24 @@ def _register_custom_op():
         return input.new_empty(B, weight.shape[0], H + 2 * padding - 2, W + 2 * padding - 2,
                                dtype=torch.float16)
 
+    # The backward is a custom op of its own: under torch.compile the
+    # autograd formula is traced with fake tensors, which have no device
+    # pointers, so the HIP calls must sit behind an op with a fake kernel.
+    @torch.library.custom_op("nova::winograd_conv2d_backward", mutates_args=())
+    def nova_winograd_conv2d_backward(grad_output: torch.Tensor, input: torch.Tensor,
+                                      weight: torch.Tensor,
+                                      padding: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        go = grad_output.contiguous()
+        holder = _op_bwd_holder(go.device)
+        with _op_lock:
+            gi = _grad_input_nova(holder, go, weight, padding, input.dtype)
+            gw = _grad_weight(holder, input, go, weight, padding)
+        return gi, gw
+
+    @nova_winograd_conv2d_backward.register_fake
+    def _(grad_output, input, weight, padding):
+        return torch.empty_like(input), torch.empty_like(weight)
+
     def _keep(ctx, inputs, output):
         input, weight, padding, bias = inputs
         ctx.save_for_backward(input, weight)
@@ -373,10 +391,9 @@ def _register_custom_op():
 
     def _grads(ctx, grad_output):
         input, weight = ctx.saved_tensors
-        go = grad_output.contiguous()
-        gi = _grad_input_nova(_op_bwd_holder(go.device), go, weight, ctx.padding, input.dtype)
-        gw = _grad_weight(_op_bwd_holder(go.device), input, go, weight, ctx.padding)
-        gb = None if ctx.bias_dtype is None else go.float().sum(dim=(0, 2, 3)).to(ctx.bias_dtype)
+        gi, gw = torch.ops.nova.winograd_conv2d_backward(grad_output, input, weight, ctx.padding)
+        gb = (None if ctx.bias_dtype is None
+              else grad_output.float().sum(dim=(0, 2, 3)).to(ctx.bias_dtype))
         return gi, gw, None, gb
 
     nova_winograd_conv2d.register_autograd(_grads, setup_context=_keep)
