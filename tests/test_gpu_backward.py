@@ -128,12 +128,33 @@ def test_grad_input_follows_weight_updates():
 
 
 # (B, C, K, H, W, pad): edge tiles, K and C off the 64-blocks, pads 0-2,
-# non-square, the ResNet-50 layers at B=1 and B=32 and one multi-sub-batch case
+# non-square, the ResNet-50 layers at B=1 and B=32, a stem-like 3 -> 64 layer
+# at 224^2, and one batch the library splits into sub-batches: at 3 -> 64 on
+# 224^2 (1 444 tiles per image) a sub-batch holds at most 43 images (Vt and Mt
+# together within 1 GiB), so batch 44 runs as 43 + 1 images and the second
+# sub-batch adds into the first one's filter gradient (the accumulate pass of
+# wg_gemm_proj_kernel, with the tile range split over the CUs)
 WGRAD_CASES = [
     (2, 16, 24, 14, 14, 1), (1, 32, 8, 11, 11, 0), (2, 8, 16, 9, 9, 2), (3, 40, 72, 13, 17, 1),
     (1, 64, 64, 56, 56, 1), (1, 512, 512, 7, 7, 1), (32, 64, 64, 56, 56, 1),
-    (32, 256, 256, 14, 14, 1), (2, 3, 64, 224, 224, 1),
+    (32, 256, 256, 14, 14, 1), (2, 3, 64, 224, 224, 1), (44, 3, 64, 224, 224, 1),
 ]
+
+
+def wgrad_chunk_images(B, C, K, H, W, pad):
+    """Images per sub-batch of nova_weight_grad (the library's rule: Vt and Mt
+    in fp32, 256 bytes per channel and tile, each below 2^31 bytes and
+    together within 1 GiB)."""
+    P = -(-(H + 2 * pad - 2) // 6) * -(-(W + 2 * pad - 2) // 6)
+    per_img = 256 * P
+    by_off = ((1 << 31) - 256 * 16 - 1) // (per_img * max(C, K))
+    by_total = (1 << 30) // (per_img * (C + K))
+    return max(1, min(max(B, 1), by_off, by_total))
+
+
+def test_wgrad_cases_include_a_split_batch():
+    assert wgrad_chunk_images(44, 3, 64, 224, 224, 1) == 43
+    assert any(wgrad_chunk_images(*c) < c[0] for c in WGRAD_CASES)
 
 
 @pytest.mark.parametrize("B,C,K,H,W,pad", WGRAD_CASES)
