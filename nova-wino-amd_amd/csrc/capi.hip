@@ -89,7 +89,8 @@ struct Profiler {
     void done(int kind, size_t e0, const char* name) {
         names[kind] = name;
         if (e0 == SIZE_MAX) return;
-        if (kernel_events().start != nullptr) {  // nothing was launched
+        if (kernel_events().start != nullptr || kernel_events().stop != nullptr) {
+            // a launch did not take its events: no span
             kernel_events() = KernelEvents{};
             return;
         }
@@ -762,20 +763,29 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             }
             const bool nhwc = Hd->nhwc != 0;
             auto fz = [=]() {
+                // a timed forward: one span from the tile-block kernel's start
+                // to the tail launch's end
+                const KernelEvents ev = kernel_events();
+                if (tail > 0 && ev.start != nullptr) kernel_events() = KernelEvents{ev.start, nullptr};
                 hipError_t e = launch_fused_block(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad,
                                                   s.nh, s.nw, s.Ho, s.Wo, bp, st, ep);
-                if (e == hipSuccess && tail > 0)
+                if (e == hipSuccess && tail > 0) {
+                    if (ev.start != nullptr) kernel_events() = KernelEvents{nullptr, ev.stop};
                     e = launch_fused_small(xx, U, yy, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw,
                                            s.Ho, s.Wo, sp, st, ep, nhwc);
+                }
                 return e;
             };
             if (b0 == 0 && !no_alloc) {
                 for (int k = 0; k < kNumKinds; k++) pf.last[k] = nullptr;
                 pf.last[kKindFused] = fz;
             }
+            // with the tail launch the span covers both kernels, and its name
+            // says so (per-kernel times and byte models can tell them apart)
             const size_t e0 = no_alloc ? SIZE_MAX : pf.arm();
             const bool ok = hip_ok(fz(), "fused block kernel");
-            pf.done(kKindFused, e0, "fused_block_kernel");
+            pf.done(kKindFused, e0,
+                    tail > 0 ? "fused_block_kernel+fused_small_kernel" : "fused_block_kernel");
             if (!ok) return;
         } else if (path == 2) {
             const hipStream_t st = Hd->stream;

@@ -13,8 +13,9 @@ namespace nova {
 // and end (the timestamps of its dispatch packet, hipExtLaunchKernelGGL) into
 // those events, which then time the kernel alone -- without the dispatch gap
 // in front of it that events recorded between kernels would include. The
-// events are consumed by that launch. Unset (the default), launches are plain
-// triple-chevron launches.
+// events are consumed by that launch; either may be null (a span over two
+// launches: the first records the start, the second the end). Unset (the
+// default), launches are plain triple-chevron launches.
 struct KernelEvents {
     hipEvent_t start = nullptr, stop = nullptr;
 };
@@ -25,7 +26,7 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t 
                    Args... args) {
     static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
     KernelEvents& ev = kernel_events();
-    if (ev.start != nullptr) {
+    if (ev.start != nullptr || ev.stop != nullptr) {
         hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev.start, ev.stop, 0,
                               static_cast<KArgs>(args)...);
         ev = KernelEvents{};

@@ -21,7 +21,7 @@ DEV = torch.device("cuda:0")
 CL = torch.channels_last
 
 
-def _forward(lib, x, w, pad, nhwc=False, bias=None, relu=0):
+def _forward(lib, x, w, pad, nhwc=False, bias=None, relu=0, names=None):
     from nova_winograd.ops import check
 
     B, C, H, W = x.shape
@@ -37,16 +37,23 @@ def _forward(lib, x, w, pad, nhwc=False, bias=None, relu=0):
         lib.nova_set_weights(h, w.data_ptr(), K, C)
         if bias is not None or relu:
             lib.nova_set_epilogue(h, bias.data_ptr() if bias is not None else None, relu)
+        if names is not None:
+            lib.nova_profile_enable(h, 1)
         lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, W, pad)
         check("forward")
         assert lib.nova_get_last_path(h) == 3
         torch.cuda.synchronize()
+        if names is not None:
+            # the fused kind's span names the tail launch when it ran
+            names.append(lib.nova_profile_kernel_name(h, 3).decode())
+            lib.nova_profile_enable(h, 0)
     finally:
         lib.nova_destroy(h)
     return y
 
 
-# (B, C, K, H, pad); on 256 CUs every case splits
+# (B, C, K, H, pad); on 256 CUs every case splits (asserted through the
+# profiler's name for the fused span), and no batch of eight does
 CASES = [
     (40, 64, 64, 56, 1),    # conv2_x: 280 workgroups, 240 full runs
     (37, 48, 64, 56, 1),    # 259 workgroups, 222 full runs, 48 input channels
@@ -71,12 +78,19 @@ def test_fused_tail_matches_chunks(oracle, B, C, K, H, pad, nhwc):
     xd, wd = x.to(DEV), w.to(DEV)
     if nhwc:
         xd = xd.contiguous(memory_format=CL)
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
     for epi in (False, True):
         b_, r_ = (bias, 1) if epi else (None, 0)
-        y = _forward(lib, xd, wd, pad, nhwc, b_, r_).contiguous().cpu()
+        names, part_names = [], []
+        y = _forward(lib, xd, wd, pad, nhwc, b_, r_, names).contiguous().cpu()
         assert torch.isfinite(y.float()).all()
-        parts = [_forward(lib, xd[i:i + 8], wd, pad, nhwc, b_, r_).contiguous().cpu()
+        parts = [_forward(lib, xd[i:i + 8], wd, pad, nhwc, b_, r_, part_names).contiguous().cpu()
                  for i in range(0, B, 8)]
+        print(f"[fused tail] {cus} CUs: batch ran {names[0]}, chunks {set(part_names)}",
+              flush=True)
+        assert all(n == "fused_block_kernel" for n in part_names)
+        if cus == 256:  # the CU count these batches were chosen for
+            assert names[0] == "fused_block_kernel+fused_small_kernel"
         assert torch.equal(y.view(torch.int16), torch.cat(parts).view(torch.int16))
         if not epi:
             # the parity bar for unit-scale outputs: rel-L2 5e-3, max-abs 0.5
