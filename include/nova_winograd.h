@@ -184,12 +184,15 @@ NOVA_API int nova_get_last_path(nova_handle_t h);
 
 /* No counterpart in the reference. nova_forward for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc. Same result as nova_forward on the same
- * handle, bit for bit, and nothing is allocated: the three-pass workspace is a
- * scratch array of NOVA_NOALLOC_SCRATCH_BYTES compiled into the library (one
- * copy per GPU, held until the process ends), batches are split so every
- * launch fits it, and a shape whose single image needs more workspace than
- * that is refused (error 4, output untouched). Every call on a GPU shares that
+ * harnesses that forbid hipMalloc. Nothing is allocated: the three-pass
+ * workspace is a scratch array of NOVA_NOALLOC_SCRATCH_BYTES compiled into
+ * the library (one copy per GPU, held until the process ends), batches are
+ * split so every launch fits it, and a shape whose single image needs more
+ * workspace than that is refused (error 4, output untouched). The result is
+ * nova_forward's bit for bit when both run the same sub-batches; where the
+ * scratch splits a batch that nova_forward runs whole, the GEMM's tile
+ * follows the smaller launch and the outputs agree within fp32 accumulation
+ * order (the same rounding points, M summed in another order). Every call on a GPU shares that
  * GPU's scratch: calls that overlap on one GPU (unordered streams, other host
  * threads) race. The position-row fused path needs allocated scratch and is
  * never taken here (a forced path 2 runs three-pass and reports it), and these
