@@ -21,9 +21,9 @@ Reported on one JSON line (stdout):
                timed live: every kernel records its own start and end events
                (its dispatch packet, on its launch stream) over a timed region
                of K steps; algorithmic bytes per launch / average launch time
-               vs 8 TB/s (frac, warm: the steady-state loop), and the same
-               launches in cold forwards (frac_cold: a 512 MiB write before
-               each forward, so x and U come from HBM)
+               vs 8 TB/s in cold forwards (frac: a 512 MiB write before each
+               forward, so x and U come from HBM), with the warm steady-state
+               loop's figures beside them (frac_warm)
   cpu_baseline the CPU oracle (the reference's NOVA arithmetic, C, OpenMP) on
                a bounded sample of the same layers, on this host's cores
 
@@ -448,8 +448,12 @@ def kernel_stats_from(trace_dir, bench_json, out_path):
               "pair also holds each dispatch's wait behind the kernel before it (the barrier "
               "and cache flush between dependent launches), which the trace leaves out: about "
               "0.1-1.3 us per launch, so the ratio runs from 1.0 to 1.3 with the box.", "",
-              "| family | bench avg_launch_us | rocprofv3 mean us | calls | ratio |",
-              "|---|---:|---:|---:|---:|"]
+              "Fractions of 8 TB/s use the family's algorithmic bytes per launch (the bench "
+              "line's achieved GB/s x its event-timed launch) over each duration: the bench's "
+              "warm and cold event times, and the trace's warm End - Start.", "",
+              "| family | bench avg_launch_us | rocprofv3 mean us | calls | ratio | "
+              "alg MB/launch | frac (events, warm) | frac (trace, warm) | frac (events, cold) |",
+              "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
     fams = line.get("kernel_families", {})
     for fam, rec in fams.items():
         keys = KERNEL_FAMILY.get(fam, (fam,))
@@ -457,13 +461,18 @@ def kernel_stats_from(trace_dir, bench_json, out_path):
         if not d:
             continue
         m = statistics.mean(d)
+        alg = rec["achieved_gbs"] * rec["avg_launch_us"] * 1e3  # bytes per launch
         lines.append(f"| {fam} | {rec['avg_launch_us']:.3f} | {m:.3f} | {len(d)} | "
-                     f"{rec['avg_launch_us'] / m:.3f} |")
+                     f"{rec['avg_launch_us'] / m:.3f} | {alg / 1e6:.2f} | "
+                     f"{rec['frac_hbm']:.4f} | {alg / (m * 1e-6) / 1e9 / PEAK_HBM_GBS:.4f} | "
+                     f"{rec.get('frac_hbm_cold', float('nan')):.4f} |")
     rl = line["roofline"]
+    warm = (f"; warm loop {rl['avg_launch_us_warm']} us, {rl['frac_warm']}"
+            if "frac_warm" in rl else "")
     lines += ["", f"Dominant family in the bench line: `{rl['kernel']}`, avg_launch_us = "
-                  f"{rl['avg_launch_us']}, achieved {rl['achieved']} GB/s = {rl['frac']} of "
-                  f"{rl['peak']} GB/s (bench value {line['value']} TFLOP/s, "
-                  f"{line['ms_per_step']} ms per step)."]
+                  f"{rl['avg_launch_us']} ({rl.get('cache', 'warm')}), achieved "
+                  f"{rl['achieved']} GB/s = {rl['frac']} of {rl['peak']} GB/s{warm} "
+                  f"(bench value {line['value']} TFLOP/s, {line['ms_per_step']} ms per step)."]
     with open(out_path, "w") as f:
         f.write("\n".join(lines) + "\n")
     print(f"wrote {out_path}")
@@ -924,24 +933,28 @@ def main():
     bytes_per_launch = dom["bytes"] / dom["launches"]  # launches: one per layer per step
     achieved = bytes_per_launch / avg_s / 1e9
     dom_desc = ",".join(sorted(set(dom["by_layer"])))
+    # Headline fraction = cold launches (a 512 MiB write before each forward,
+    # so x and U come from HBM; see cold_measurements): at these sizes a warm
+    # loop keeps U in the 256 MB memory-side cache and can read above the HBM
+    # roofline. The warm steady-state figures (the ones a kernel trace of the
+    # same loop reproduces) stay beside them.
+    avg_cold_s = dom["ms_cold"] / dom["launches"] * 1e-3
+    achieved_cold = bytes_per_launch / avg_cold_s / 1e9
     roofline = {
         "bound": "hbm",
-        "achieved": round(achieved, 1),
+        "achieved": round(achieved_cold, 1),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
-        "frac": round(achieved / PEAK_HBM_GBS, 4),
+        "frac": round(achieved_cold / PEAK_HBM_GBS, 4),
         "traffic": load_traffic(dom_name),
         "kernel": dom_name,
-        "avg_launch_us": round(avg_s * 1e6, 3),
+        "avg_launch_us": round(avg_cold_s * 1e6, 3),
         "timing": "hipEvents recorded by each kernel's dispatch packet over a timed region of K steps",
+        "cache": "cold (512 MiB write before each forward)",
+        "avg_launch_us_warm": round(avg_s * 1e6, 3),
+        "achieved_warm": round(achieved, 1),
+        "frac_warm": round(achieved / PEAK_HBM_GBS, 4),
         "replay_avg_launch_us": round(dom["replay_ms"] / dom["launches"] * 1e3, 3),
-        # the same launches in cold forwards (x and U from HBM; see
-        # cold_measurements): the cold fraction beside the warm one above
-        "avg_launch_us_cold": round(dom["ms_cold"] / dom["launches"] * 1e3, 3),
-        "achieved_cold": round(bytes_per_launch / (dom["ms_cold"] / dom["launches"] * 1e-3)
-                               / 1e9, 1),
-        "frac_cold": round(bytes_per_launch / (dom["ms_cold"] / dom["launches"] * 1e-3)
-                           / 1e9 / PEAK_HBM_GBS, 4),
         "members": dom["members"],
         "alg_bytes_per_launch": round(bytes_per_launch),
         "launches_per_step": dom["launches"],

@@ -130,15 +130,22 @@ def test_bench_kernel_stats_summary(tmp_path):
     line = {"value": 1.0, "ms_per_step": 0.1,
             "roofline": {"kernel": "wgemm", "avg_launch_us": 11.0, "achieved": 1.0, "frac": 0.1,
                          "peak": 8000.0},
-            "kernel_families": {"wgemm": {"avg_launch_us": 11.0},
-                                "input_transform_kernel": {"avg_launch_us": 5.5}}}
+            "kernel_families": {"wgemm": {"avg_launch_us": 11.0, "achieved_gbs": 4000.0,
+                                          "frac_hbm": 0.5, "frac_hbm_cold": 0.25},
+                                "input_transform_kernel": {"avg_launch_us": 5.5,
+                                                           "achieved_gbs": 800.0,
+                                                           "frac_hbm": 0.1,
+                                                           "frac_hbm_cold": 0.05}}}
     bl = tmp_path / "line.json"
     bl.write_text("log line\n" + json.dumps(line) + "\n")
     out = tmp_path / "summary.md"
     bench.kernel_stats_from(str(trace), str(bl), str(out))
     text = out.read_text()
-    assert "| wgemm | 11.000 | 10.000 | 4 | 1.100 |" in text
-    assert "| input_transform_kernel | 5.500 | 5.000 | 4 | 1.100 |" in text
+    # 4000 GB/s x 11 us = 44 MB per launch; over the trace's 10 us: 4.4 TB/s = 0.55
+    assert "| wgemm | 11.000 | 10.000 | 4 | 1.100 | 44.00 | 0.5000 | 0.5500 | 0.2500 |" in text
+    # 800 GB/s x 5.5 us = 4.4 MB; over 5 us: 0.88 TB/s = 0.11
+    assert ("| input_transform_kernel | 5.500 | 5.000 | 4 | 1.100 | 4.40 | 0.1000 | 0.1100 | "
+            "0.0500 |") in text
 
 
 def test_bench_mfma_summary(tmp_path):
