@@ -54,7 +54,7 @@ PEAK_FP16_TFLOPS = 2500.0
 KIND_NAMES = ["input", "gemm", "output", "fused"]
 GRAPH_CALLS = 10  # forwards captured per layer graph (per-layer GPU time)
 PATH_NAMES = {1: "3-pass", 2: "fused_rows", 3: "fused_block", 4: "windowed", 5: "fused_small",
-              6: "two_pass"}
+              6: "two_pass", 7: "in_gemm"}
 
 
 def log(*a):
@@ -78,7 +78,9 @@ def kernel_alg_bytes(kind, B, C, K, H, name=""):
     input transform reads x, writes V; GEMM reads U and V, writes M; output
     transform reads M, writes y; fused reads x and U, writes y -- except the
     two-pass path's second kernel (gemm_out_kernel), which reads V and U and
-    writes y. Minimal tiling P = ceil(Ho/6)^2, channel pitch C rounded up to 8."""
+    writes y, and the input transform fused into the products (in_gemm_kernel,
+    the GEMM kind of path 7), which reads x and U and writes M. Minimal tiling
+    P = ceil(Ho/6)^2, channel pitch C rounded up to 8."""
     Cp = (C + 7) // 8 * 8
     Ho = H
     BP = B * (-(-Ho // 6)) ** 2
@@ -86,6 +88,8 @@ def kernel_alg_bytes(kind, B, C, K, H, name=""):
     V, M, U = 2 * 64 * Cp * BP, 2 * 64 * K * BP, 2 * 64 * K * Cp
     if kind == "fused" and name.startswith("gemm_out"):
         return V + U + y
+    if kind == "gemm" and name.startswith("in_gemm"):
+        return x + U + M
     return {"input": x + V, "gemm": U + V + M, "output": M + y, "fused": x + U + y}[kind]
 
 
@@ -187,11 +191,21 @@ KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_
                                             "input_nhwc_kernel"),
                  "wgemm": ("wgemm_kernel", "wgemm_lds_kernel", "wgemm_block_kernel"),
                  "output_transform_kernel": ("output_transform_kernel", "output_lp_kernel",
-                                             "output_nhwc_kernel")}
+                                             "output_nhwc_kernel"),
+                 "in_gemm_kernel": ("in_gemm_kernel",)}
 FAMILY_OF_KIND = {0: "input_transform_kernel", 1: "wgemm", 2: "output_transform_kernel"}
 
+
+def family_of(kind, kname):
+    """Kernel family of a profiled launch: its stage's family, except the
+    input transform fused into the products (path 7), a family of its own."""
+    if kname.startswith("in_gemm"):
+        return "in_gemm_kernel"
+    return FAMILY_OF_KIND.get(kind, kname)
+
 NOVA_KERNELS = ["input_transform_kernel", "wgemm", "output_transform_kernel",
-                "fused_block_kernel", "fused_small_kernel", "gemm_out_kernel", "fused_kernel<1>",
+                "fused_block_kernel", "fused_small_kernel", "gemm_out_kernel", "in_gemm_kernel",
+                "fused_kernel<1>",
                 "fused_kernel<2>", "fused_kernel<4>"]
 
 
@@ -257,7 +271,7 @@ def mfma_from(pmc_dir, bench_json, out_path, cus=256):
                       f"{CLOCK_GHZ} GHz x {cus} CUs x 4 SIMDs)",
             "peak_tflops": PEAK_FP16_TFLOPS, "clock_ghz": CLOCK_GHZ, "kernels": []}
     for name in ("wgemm", "fused_block_kernel", "fused_small_kernel", "gemm_out_kernel",
-                 "fused_kernel<1>", "fused_kernel<2>", "fused_kernel<4>"):
+                 "in_gemm_kernel", "fused_kernel<1>", "fused_kernel<2>", "fused_kernel<4>"):
         sel = {c: [r for r in per[c] if any(k in r[0] for k in _name_keys(name))]
                for c in MFMA_COUNTERS}
         mops = sel["SQ_INSTS_VALU_MFMA_MOPS_F16"]
@@ -892,7 +906,7 @@ def main():
                 r["kernels"][KIND_NAMES[k]] = {"kernel": kname, "avg_us": ev * 1e3,
                                               "replay_us": per * 1e3, "alg_bytes": ab,
                                               "gbs": ab / (ev * 1e-3) / 1e9}
-                fam = FAMILY_OF_KIND.get(k, kname)
+                fam = family_of(k, kname)
                 agg = kernels.setdefault(fam, {"ms": 0.0, "replay_ms": 0.0, "launches": 0,
                                                "bytes": 0.0, "flops": 0.0, "by_layer": [],
                                                "members": {}, "ms_cold": 0.0})

@@ -138,7 +138,13 @@ NOVA_API void nova_set_stream(nova_handle_t h, void* stream);
  * two workgroups per CU, e.g. batch 1), 6 = force the two-pass path (the
  * input transform, then the 64 products and the output transform in one
  * launch of 16 tiles x 32 output channels per workgroup, M kept on chip;
- * bit-identical to 3-pass), 4 = windowed 3-pass: the batch
+ * bit-identical to 3-pass), 7 = force the input transform fused into the
+ * products (few tiles: at most 64 per sub-batch, at most 512 input channels,
+ * pads up to 4; each workgroup builds the row of the transformed input its
+ * products need from x, M goes to memory and the output transform follows:
+ * two launches instead of three, bit-identical to 3-pass; chosen
+ * automatically for at most 32 tiles and 128 output channels, e.g. batch 1
+ * at ResNet-50 conv3_x), 4 = windowed 3-pass: the batch
  * runs in windows of whole images whose V + M fit the window budget
  * (nova_set_window_bytes), each window's three kernels back to back -- the
  * BP-windowed pipeline of /root/reference/tests/test_bp_tiled.hip:482-571,
@@ -195,8 +201,10 @@ NOVA_API int nova_get_last_path(nova_handle_t h);
  * order (the same rounding points, M summed in another order). Every call on a GPU shares that
  * GPU's scratch: calls that overlap on one GPU (unordered streams, other host
  * threads) race. The position-row fused path needs allocated scratch and is
- * never taken here (a forced path 2 runs three-pass and reports it), and these
- * calls are not timed by nova_profile_enable. */
+ * never taken here (a forced path 2 runs three-pass and reports it); the
+ * fused and path-7 kernels run only once a forward with allocation has built
+ * their copy of the transformed filter (else three-pass, the same bits for
+ * path 7); and these calls are not timed by nova_profile_enable. */
 #define NOVA_NOALLOC_SCRATCH_BYTES (64ll << 20)
 NOVA_API void nova_forward_noalloc(nova_handle_t h, const void* d_input, void* d_output, int batch,
                                    int H, int W, int pad);

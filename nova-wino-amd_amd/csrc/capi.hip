@@ -114,7 +114,8 @@ struct Handle {
     unsigned* cnt = nullptr;  // fused-kernel arrival counters, zero between launches
     size_t cnt_cap = 0;       // counters
     hipStream_t stream = nullptr;
-    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block, 4 windowed
+    int path_pref = 0;  // 0 auto, 1 three-pass, 2 fused rows, 3 fused block, 4 windowed,
+                        // 5 small fused, 6 two-pass, 7 input transform in the products
     int64_t window_bytes = kDefaultWindowBytes;  // V + M per window of the windowed path
     Epilogue ep;        // bias / residual / ReLU applied by every forward
     int nhwc = 0;       // 1: x and y are NHWC (channels last)
@@ -402,10 +403,35 @@ bool two_pass_wins(const Handle* Hd, const Shape& s) {
     return grid >= min_grid && grid <= Hd->cus && v_bytes <= (int64_t)20 << 20;
 }
 
+bool in_gemm_plan_for(const Handle* Hd, const Shape& s, InGemmPlan* p) {
+    const int64_t Bc = sub_batch(Hd, s);
+    return in_gemm_plan((int)Bc, Hd->C, Hd->K, Hd->Cp, s.nh, s.nw, s.pad, Hd->cus, p);
+}
+
+// The input transform fused into the products (path 7) instead of the
+// three-pass path's first two launches, for the GEMV-like shapes that the
+// block GEMM serves (every sub-batch at most 32 tiles) with at most 128
+// output channels. Every output-channel group of a position row repeats the
+// row's transform, so the fused launch pays off only with few such groups;
+// measured on MI355X (whole forwards, graph of ten, us, three-pass vs path
+// 7): ResNet-50 conv3_x batch 1 9.28 vs 8.77, DenseNet-161 192 -> 48 at
+// batch 1 28^2 9.49 vs 8.33, 14^2 8.91 vs 7.29, 7^2 8.65 vs 7.04; above 128
+// output channels it loses (conv4_x 9.32 vs 9.98, conv5_x 11.72 vs 12.34 with
+// the best plans).
+bool in_gemm_wins(const Handle* Hd, const Shape& s) {
+    InGemmPlan p;
+    const int64_t BPc = sub_batch(Hd, s) * s.nh * s.nw;
+    return Hd->K <= 128 && BPc <= 32 && in_gemm_plan_for(Hd, s, &p);
+}
+
 int choose_path(const Handle* Hd, const Shape& s) {
     if (Hd->path_pref == 1) return 1;
     if (Hd->path_pref == 4) return 4;
     if (Hd->path_pref == 6) return 6;
+    if (Hd->path_pref == 7) {
+        InGemmPlan p;
+        return in_gemm_plan_for(Hd, s, &p) ? 7 : 1;
+    }
     if (Hd->path_pref == 5) {
         FusedSmallPlan p;
         return fused_small_plan_for(Hd, s, &p) ? 5 : 1;
@@ -491,7 +517,8 @@ int choose_path(const Handle* Hd, const Shape& s) {
             return two ? 6 : 3;
         }
     }
-    return two_pass_wins(Hd, s) ? 6 : 1;
+    if (two_pass_wins(Hd, s)) return 6;
+    return in_gemm_wins(Hd, s) ? 7 : 1;
 }
 
 // Core forward on one sub-batch. V/M are workspaces large enough for it.
@@ -589,6 +616,46 @@ bool run_two_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, ui
     return ok_go;
 }
 
+// Path 7 on one sub-batch: the input transform fused into the products (M
+// to memory), then the three-pass output transform. Same M and y as
+// run_three_pass, bit for bit.
+bool run_in_gemm(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, uint16_t* M,
+                 bool remember, const Epilogue& ep, bool timed) {
+    Profiler& pf = Hd->prof;
+    const hipStream_t st = Hd->stream;
+    const int C = Hd->C, K = Hd->K, Cp = Hd->Cp;
+    const uint16_t* U = Hd->Uw;
+    const bool nhwc = Hd->nhwc != 0;
+    InGemmPlan ip;
+    if (!in_gemm_plan((int)s.B, C, K, Cp, s.nh, s.nw, s.pad, Hd->cus, &ip)) {
+        set_error(kErrInvalidArgument, "no input-transform + products plan for this sub-batch");
+        return false;
+    }
+    auto gm = [=]() {
+        return launch_in_gemm(x, U, M, s.B, C, K, Cp, s.H, s.W, s.pad, s.nh, s.nw, ip, st, nhwc);
+    };
+    auto out = [=]() {
+        return launch_output_transform(M, y, s.B, K, s.Ho, s.Wo, s.nh, s.nw, K,
+                                       (int64_t)K * s.BP, st, ep, nhwc);
+    };
+    if (remember) {
+        pf.last[kKindInput] = nullptr;
+        pf.last[kKindGemm] = gm;
+        pf.last[kKindOutput] = out;
+        pf.last[kKindFused] = nullptr;
+    }
+    // timed = false (allocation-free forwards): never arm the profiler, whose
+    // event pool may grow
+    size_t e = timed ? pf.arm() : SIZE_MAX;
+    const bool ok_gm = hip_ok(gm(), "input transform + products");
+    pf.done(kKindGemm, e, in_gemm_name(ip));
+    if (!ok_gm) return false;
+    e = timed ? pf.arm() : SIZE_MAX;
+    const bool ok_out = hip_ok(out(), "output transform");
+    pf.done(kKindOutput, e, "output_transform_kernel");
+    return ok_out;
+}
+
 // ---- scratch of the allocation-free forward (nova_forward_noalloc) -------
 // The three-pass V/M workspace for callers that cannot allocate device
 // memory. One copy per GPU, in device memory the loader reserves with the
@@ -654,7 +721,10 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     if (no_alloc) {
         // the position-row kernel needs an allocated M buffer and counters,
         // and a fragment copy not yet built would be allocated here
-        if (path == 2 || path == 6 || ((path == 3 || path == 5) && !Hd->uf_ready)) path = 1;
+        if (path == 2 || path == 6 || ((path == 3 || path == 5) && !Hd->uf_ready) ||
+            (path == 7 && (!Hd->uw_ready || 2 * (int64_t)64 * Hd->K * s_all.nh * s_all.nw >
+                                                 (int64_t)NOVA_NOALLOC_SCRATCH_BYTES)))
+            path = 1;
         const int64_t per_img = 2 * (int64_t)64 * (Hd->Cp + Hd->K) * s_all.nh * s_all.nw;
         if ((path == 1 || path == 4) && per_img > (int64_t)NOVA_NOALLOC_SCRATCH_BYTES - 256) {
             set_error(kErrWorkspace,
@@ -663,14 +733,18 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
                       fn, (long long)per_img, (long long)NOVA_NOALLOC_SCRATCH_BYTES);
             return;
         }
-        // V, then M at the next 256-byte boundary
+        // V, then M at the next 256-byte boundary (path 7: M only)
         if (path == 1 || path == 4)
             chunk = std::min<int64_t>(chunk, (NOVA_NOALLOC_SCRATCH_BYTES - 256) / per_img);
+        if (path == 7)
+            chunk = std::min<int64_t>(
+                chunk, NOVA_NOALLOC_SCRATCH_BYTES / (2 * (int64_t)64 * Hd->K * s_all.nh * s_all.nw));
     }
     const bool fused = path == 2 || path == 3 || path == 5;
     if (fused && !ensure_uf(Hd)) return;
-    if (path == 6 && !ensure_uw(Hd)) return;
-    if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3 || Hd->path_pref == 5)) {
+    if ((path == 6 || path == 7) && !ensure_uw(Hd)) return;
+    if (path == 1 && (Hd->path_pref == 2 || Hd->path_pref == 3 || Hd->path_pref == 5 ||
+                      Hd->path_pref == 7)) {
         set_error(kErrInvalidArgument, "%s: fused path unsupported for this shape; ran 3-pass", fn);
     }
     Hd->last_path = path;
@@ -684,8 +758,9 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
     const bool blocks = (path == 1 || path == 4) && !no_alloc &&
                         wgemm_blocks(Hd->K, Hd->Cp, (int)std::min<int64_t>(BPc, INT32_MAX));
     if (blocks && !ensure_uw(Hd)) return;
-    const int64_t needV = (path == 6 || blocks) ? gemm_out_v_elems(Hd->Cp, BPc)
-                                                : 64 * (int64_t)Hd->Cp * BPc;
+    const int64_t needV = path == 7 ? 0
+                          : (path == 6 || blocks) ? gemm_out_v_elems(Hd->Cp, BPc)
+                                                  : 64 * (int64_t)Hd->Cp * BPc;
     const int64_t needM = 64 * (int64_t)Hd->K * BPc;
     uint16_t* V = nullptr;
     uint16_t* M = nullptr;
@@ -694,7 +769,7 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
         M = V + ((needV + 127) & ~(int64_t)127);  // 256-byte aligned
     } else if (!fused) {
         size_t ws_bytes = 0;
-        const bool userV = V_user && needV <= V_cap && aligned16(V_user);
+        const bool userV = needV == 0 || (V_user && needV <= V_cap && aligned16(V_user));
         const bool userM = path == 6 || (M_user && needM <= M_cap && aligned16(M_user));
         if (!userV) ws_bytes += (size_t)needV * 2;
         if (!userM) ws_bytes += (size_t)needM * 2;
@@ -814,6 +889,8 @@ void forward_impl(Handle* Hd, const void* x, void* y, const Shape& s_all, void* 
             if (!ok) return;
         } else if (path == 6) {
             if (!run_two_pass(Hd, xx, yy, s, V, b0 == 0, ep)) return;
+        } else if (path == 7) {
+            if (!run_in_gemm(Hd, xx, yy, s, M, b0 == 0 && !no_alloc, ep, !no_alloc)) return;
         } else if (!run_three_pass(Hd, xx, yy, s, V, M, b0 == 0 && !no_alloc, ep, !no_alloc,
                                    blocks)) {
             return;
@@ -1114,14 +1191,14 @@ void nova_set_stream(nova_handle_t h, void* stream) {
 void nova_set_path(nova_handle_t h, int path) {
     Handle* H = as_handle(h, "nova_set_path");
     if (!H) return;
-    if (path < 0 || path > 6) {
-        set_error(kErrInvalidArgument, "nova_set_path: path must be 0, 1, 2, 3, 4, 5 or 6");
+    if (path < 0 || path > 7) {
+        set_error(kErrInvalidArgument, "nova_set_path: path must be 0 to 7");
         return;
     }
     H->path_pref = path;
     if ((path == 2 || path == 3 || path == 5) && H->ready)
         ensure_uf(H);  // fused forced after the weights
-    if (path == 6 && H->ready) ensure_uw(H);
+    if ((path == 6 || path == 7) && H->ready) ensure_uw(H);
 }
 
 void nova_set_window_bytes(nova_handle_t h, long long bytes) {
@@ -1177,6 +1254,7 @@ long long nova_workspace_bytes(nova_handle_t h, int batch, int H, int W, int pad
     if (path == 4) chunk = std::min(chunk, window_images(Hd, s));
     const int64_t BPc = std::min<int64_t>(chunk, s.B) * s.nh * s.nw;
     if (path == 6) return (long long)(gemm_out_v_elems(Hd->Cp, BPc) * 2);  // V only
+    if (path == 7) return (long long)(64 * (int64_t)Hd->K * BPc * 2);      // M only
     if (wgemm_blocks(Hd->K, Hd->Cp, (int)std::min<int64_t>(BPc, INT32_MAX)))  // V in blocks + M
         return (long long)((gemm_out_v_elems(Hd->Cp, BPc) + 64 * (int64_t)Hd->K * BPc) * 2);
     return (long long)(64 * ((int64_t)Hd->Cp + Hd->K) * BPc * 2);

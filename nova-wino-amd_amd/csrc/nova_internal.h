@@ -204,6 +204,30 @@ hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, i
                            int Cp, int nh, int nw, int Ho, int Wo, hipStream_t s, Epilogue ep,
                            bool nhwc);
 
+// Input transform fused into the products (path 7), for GEMV-like shapes
+// (few tiles, many channels): workgroup = position row x group of nt <= 16
+// tiles x kr 16-row output-channel tiles; each builds the V slice its
+// products need in LDS and writes M in the product layout [64][BP][K] (the
+// output transform follows as its own launch). U from launch_u_wfrag's
+// blocks. M equals the three-pass path's bit for bit.
+struct InGemmPlan {
+    int nt;      // tiles per workgroup
+    int ntg;     // tile groups
+    int kr;      // 16-row output-channel tiles per workgroup (1 or 2)
+    int nkg;     // output-channel groups
+    int nsteps;  // 32-channel steps
+    int nsm;     // steps the kernel instantiation holds (4, 8 or 16)
+    int64_t grid;
+};
+// False when the shape is outside the kernel's envelope (more than 64 tiles,
+// more than 512 channels, pads above 4, 32-bit offsets).
+bool in_gemm_plan(int B, int C, int K, int Cp, int nh, int nw, int pad, int cus,
+                  InGemmPlan* p);
+const char* in_gemm_name(const InGemmPlan& p);
+hipError_t launch_in_gemm(const uint16_t* x, const uint16_t* Uw, uint16_t* M, int B, int C,
+                          int K, int Cp, int H, int W, int pad, int nh, int nw,
+                          const InGemmPlan& p, hipStream_t s, bool nhwc);
+
 // ---- weight gradient (Winograd domain, fp32) --------------------------------
 // Plan of a weight-gradient computation: images per sub-batch (the fp32
 // transformed operands stay below 2^31 bytes each and 1 GiB together), the

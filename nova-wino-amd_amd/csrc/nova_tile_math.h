@@ -185,6 +185,30 @@ __device__ __forceinline__ void input_row(Load ld, float out[8]) {
     }
 }
 
+// input_row with the columns outside the image zeroed after the first pass
+// (bit j of cols clear: t[j] = +0, what all-zero inputs give, since the chain
+// starts at +0), so ld(i, j) may return anything for such a column.
+template <int I, typename Load>
+__device__ __forceinline__ void input_row_masked(Load ld, unsigned cols, float out[8]) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (kBh[i][I] != 0.0f) acc = __builtin_fmaf(kBh[i][I], ld(i, j), acc);
+        t[j] = ((cols >> j) & 1u) ? acc : 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (kBh[j][s] != 0.0f) acc = __builtin_fmaf(t[j], kBh[j][s], acc);
+        out[s] = acc;
+    }
+}
+
 // True when input row i enters row I of V (B[i][I] != 0).
 constexpr bool input_row_uses(int I, int i) { return kBh[i][I] != 0.0f; }
 

@@ -71,7 +71,7 @@ def test_handle_lifecycle_and_errors(lib):
     assert lib.nova_get_last_error() == 0  # cleared
     lib.nova_forward(h, 1, 2, 1, 8, 8, 1)  # weights never set: refused before any GPU work
     assert lib.nova_get_last_error() == 2
-    lib.nova_set_path(h, 7)
+    lib.nova_set_path(h, 8)
     assert lib.nova_get_last_error() == 1
     lib.nova_set_path(h, 1)
     assert lib.nova_get_last_error() == 0

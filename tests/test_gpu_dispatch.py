@@ -90,6 +90,10 @@ AUTO_CASES = [
     (1, 64, 64, 112, 5),   # 724 workgroups: 13.3 vs 14.9 us
     (2, 64, 64, 112, 6),   # 1448 workgroups: small kernel 21.4 vs two-pass 16.2 us
     (32, 48, 40, 13, 5),   # small images: 480 workgroups
+    (1, 128, 128, 28, 7),  # conv3_x B=1: input transform in the products, 8.8 vs 9.3 us
+    (1, 192, 48, 14, 7),   # DenseNet-161 bottleneck B=1: 7.3 vs 8.9 us
+    (1, 256, 256, 14, 1),  # conv4_x B=1: above 128 output channels, three-pass
+    (1, 512, 512, 7, 1),   # conv5_x B=1
 ]
 
 
@@ -108,7 +112,7 @@ def test_auto_path_matches_three_pass(oracle, B, C, K, H, expect):
     a = y_auto.float().cpu().numpy()
     r = y_3p.float().cpu().numpy()
     assert np.isfinite(a).all()
-    if expect in (1, 6):  # the two-pass path is three-pass arithmetic
+    if expect in (1, 6, 7):  # two-pass and path 7 are three-pass arithmetic
         assert np.array_equal(y_auto.cpu().view(torch.int16).numpy(),
                               y_3p.cpu().view(torch.int16).numpy())
     else:
@@ -125,13 +129,15 @@ def test_auto_path_matches_three_pass(oracle, B, C, K, H, expect):
     assert oracle.rel_l2(a[:2].astype(np.float16), yo) <= 5e-3
 
 
-@pytest.mark.parametrize("path", [1, 3, 5, 6], ids=["3pass", "fused_block", "fused_small", "two_pass"])
+@pytest.mark.parametrize("path", [1, 3, 5, 6, 7],
+                         ids=["3pass", "fused_block", "fused_small", "two_pass", "in_gemm"])
 def test_graph_replay_matches_eager(path):
     """A forward captured in a HIP graph replays to the eager result, with
     eager work and synchronisation between replays."""
     print(f"[graph] path={path}", flush=True)
     lib = _lib()
-    B, C, K, H = 8, 64, 64, 56
+    # path 7 serves few tiles (at most 64): batch 1 at conv3_x
+    B, C, K, H = (1, 128, 128, 28) if path == 7 else (8, 64, 64, 56)
     torch.manual_seed(3)
     x = torch.randn(B, C, H, H, device=DEV).half()
     w = _kaiming(K, C).to(DEV)

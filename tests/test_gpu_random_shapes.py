@@ -3,11 +3,11 @@
 Forty small layers drawn from one seed (batch 1-6, 1-160 input and output
 channels, images 1x1 to 40x40 including non-square ones, pad 0-2) run through
 the automatic choice and each forced path (three-pass, fused rows, fused
-tile-block, small-problem fused, two-pass, windowed), NCHW and, for C % 8 ==
-0, channels-last. Every output is finite and within the reference's
-tolerance of the oracle; three-pass, two-pass and windowed agree bit for bit
-(the same arithmetic); a forced fused path either runs or reports that it
-fell back to three-pass. The shapes cover edges the hand-picked cases may
+tile-block, small-problem fused, two-pass, windowed, the input transform in
+the products), NCHW and, for C % 8 == 0, channels-last. Every output is
+finite and within the reference's tolerance of the oracle; three-pass,
+two-pass, windowed and path 7 agree bit for bit (the same arithmetic); a
+forced fused path either runs or reports that it fell back to three-pass. The shapes cover edges the hand-picked cases may
 miss: one-tile images, channel counts off every 8/16/32 block, K below 16,
 tiles past an image edge in every position of a tile block.
 """
@@ -60,7 +60,7 @@ def _run(lib, x, w, pad, path, nhwc=False):
         lib.nova_forward(h, x.data_ptr(), y.data_ptr(), B, H, W, pad)
         took = lib.nova_get_last_path(h)
         torch.cuda.synchronize()
-        if path in (2, 3, 5) and took == 1:
+        if path in (2, 3, 5, 7) and took == 1:
             # a forced fused path outside its envelope runs three-pass and says so
             assert lib.nova_get_last_error() != 0
         else:
@@ -83,7 +83,7 @@ def test_random_shape_all_paths(oracle, B, C, K, H, W, pad):
     n = min(B, 2)
     yo = oracle.conv2d(x[:n].numpy(), w.numpy(), pad)
     outs = {}
-    for path in (0, 1, 2, 3, 4, 5, 6):
+    for path in (0, 1, 2, 3, 4, 5, 6, 7):
         y, took = _run(lib, xd, wd, pad, path)
         yc = y.cpu()
         a = yc.float().numpy()
@@ -92,12 +92,12 @@ def test_random_shape_all_paths(oracle, B, C, K, H, W, pad):
         assert oracle.max_abs(a[:n].astype(np.float16), yo) <= 0.25, (path, took)
         outs[path] = (yc, took)
     y1 = outs[1][0]
-    for path in (4, 6):  # same arithmetic as three-pass
+    for path in (4, 6, 7):  # same arithmetic as three-pass
         assert torch.equal(outs[path][0], y1), path
     if C % 8 == 0:
         # channels-last: the same kernels' arithmetic, so the same bits per path
         xc = xd.contiguous(memory_format=CL)
-        for path in (0, 1, 6):
+        for path in (0, 1, 6, 7):
             y, took = _run(lib, xc, wd, pad, path, nhwc=True)
             ref, took_ref = outs[path]
             if took == took_ref:

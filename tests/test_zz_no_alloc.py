@@ -60,7 +60,8 @@ CASES = [
     (128, 128, 28, 1, 8, 3, 1),     # three-pass, conv3_x
     (64, 64, 56, 1, 32, 24, 3),     # fused tile-block, conv2_x (no workspace)
     (512, 512, 7, 1, 32, 1, 1),     # three-pass, conv5_x, then batch 1
-    (100, 24, 17, 0, 6, 2, 1),      # C % 8 != 0 (padded channel pitch), pad 0
+    (100, 24, 17, 0, 6, 2, (1, 7)),  # C % 8 != 0 (padded channel pitch), pad 0; batch 2
+                                     # takes the input transform in the products (M only)
     (40, 24, 17, 0, 6, 2, 5),       # the small-problem fused kernel (no workspace)
 ]
 
@@ -74,10 +75,10 @@ def test_noalloc_equals_forward_twice(C, K, H, pad, B1, B2, path):
     h = lib.nova_create()
     try:
         lib.nova_set_weights(h, w.data_ptr(), K, C)
-        for B in (B1, B2):
+        for B, want in zip((B1, B2), path if isinstance(path, tuple) else (path, path)):
             x = torch.randn(B, C, H, H, device=DEV).half()
             y_ref, y, p_ref, p = _pair(lib, h, x, K, pad)
-            assert p == p_ref == path, (p, p_ref)
+            assert p == p_ref == want, (p, p_ref)
             assert torch.equal(y, y_ref), f"B={B}"
     finally:
         lib.nova_destroy(h)
@@ -103,10 +104,12 @@ def test_noalloc_channels_last_with_epilogue():
             res = torch.randn(B, K, H, H, device=DEV).half().contiguous(
                 memory_format=torch.channels_last)
             lib.nova_set_residual(h, res.data_ptr())
-            y_ref, y, _, p = _pair(lib, h, x, K, 1, nhwc=True)
+            y_ref, y, p_ref, p = _pair(lib, h, x, K, 1, nhwc=True)
             lib.nova_set_residual(h, None)
             check()
-            assert p == 1
+            # batch 2 (32 tiles, 96 output channels): the input transform in
+            # the products, M in the scratch
+            assert p == p_ref == (1 if B == 6 else 7), (p, p_ref)
             assert torch.equal(y, y_ref), f"B={B}"
     finally:
         lib.nova_destroy(h)
