@@ -537,6 +537,141 @@ static int pick_tw(int64_t rows, int n, int ch) {
     return widest_g < 256 ? widest : best;
 }
 
+// ---------------------------------------------------------------------------
+// Input transform into the two-pass block layout, run form. The tile-block
+// kernel above covers tiles of one tile row, so each 128-byte line of a V
+// block (8 consecutive tiles x 8 channels of one position) collects its
+// 16-byte pieces from several workgroups and has to merge in the L2. Here a
+// workgroup takes 16 consecutive tiles (bp, across tile rows and images:
+// one block column) x 16 channels; wave w holds tiles 8*(w & 1) .. +7 x
+// channels 8*(w >> 1) .. +7 of them, lane = (tile % 8, channel % 8), so each
+// store instruction writes one whole line of a position's block (streamed
+// past the L2 when kStream). Each thread loads its patch's 8 rows straight
+// from global memory (a 16-byte and a 4-byte load from the dword at or below
+// the row start, shifted by 0 or 2 bytes; rows outside the image and
+// channels past C read zero; a row starting before x_al, only the tensor's
+// first row with left padding, is loaded from 0 and shifted into place),
+// masks the columns outside the image and runs the shared chains: V is the
+// tile-block kernel's, bit for bit. NCHW only.
+// ---------------------------------------------------------------------------
+template <bool kStream>
+__global__ __launch_bounds__(256) void input_run_kernel(
+    const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int Cp, int H, int W,
+    int pad, int nw, int P, int BP, int ncg, int vfrag, int64_t pstride, int x_bytes, int xd,
+    int64_t v_bytes) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int cg = L % ncg, blk = L / ncg;
+    const int c = cg * 16 + 8 * (wave >> 1) + (lane & 7);
+    const int t = 8 * (wave & 1) + (lane >> 3);
+    const int bp = blk * 16 + t;
+    if (bp >= BP || c >= Cp) return;  // nothing to store (no barrier in this kernel)
+    const int b = bp / P, tr = bp - (bp / P) * P;
+    const int th = tr / nw, tw = tr - (tr / nw) * nw;
+    const int h0 = 6 * th - pad, w0 = 6 * tw - pad;
+    const int HW = H * W;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x_al, x_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(V, v_bytes);
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    unsigned w5[8][5];
+    unsigned odd = 0, neg = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int h = h0 + i;
+        const bool ok = c < C && h >= 0 && h < H;
+        const int o = xd + 2 * ((b * C + c) * HW + h * W + w0);
+        odd |= (unsigned)((o >> 1) & 1) << i;
+        neg |= (ok && o < 0) ? (1u << i) : 0u;
+        const int A = !ok ? kOob : (o < 0 ? 0 : (o & ~3));
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, A, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) w5[i][q] = v[q];
+        w5[i][4] = __builtin_amdgcn_raw_buffer_load_b32(xrs, A + 16, 0, 0);
+    }
+    if (neg != 0) {
+        // rows loaded from 0 instead of up to 8 bytes (pads up to 4) before
+        // x_al: move their dwords up by the missing ones (the zeros land in
+        // masked columns)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (!((neg >> i) & 1u)) continue;
+            const int o = xd + 2 * ((b * C + c) * HW + (h0 + i) * W + w0);
+            const int sh = -(o >> 2);
+            unsigned l5[5];
+#pragma unroll
+            for (int q = 0; q < 5; q++) l5[q] = w5[i][q];
+#pragma unroll
+            for (int q = 0; q < 5; q++) {
+                unsigned v = 0;
+#pragma unroll
+                for (int rr = 0; rr < 5; rr++) v = (q - sh == rr) ? l5[rr] : v;
+                w5[i][q] = v;
+            }
+        }
+    }
+    unsigned cmask = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int w = w0 + j;
+        cmask |= (w >= 0 && w < W) ? (1u << j) : 0u;
+    }
+    unsigned d4[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const unsigned sb = ((odd >> i) & 1u) * 2;
+#pragma unroll
+        for (int q = 0; q < 4; q++) d4[i][q] = __builtin_amdgcn_alignbyte(w5[i][q + 1], w5[i][q], sb);
+    }
+    if (cmask != 0xffu) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const unsigned m = (((cmask >> (2 * q)) & 1u) ? 0xffffu : 0u) |
+                               (((cmask >> (2 * q + 1)) & 1u) ? 0xffff0000u : 0u);
+#pragma unroll
+            for (int i = 0; i < 8; i++) d4[i][q] &= m;
+        }
+    }
+    const int voff = v_plane_off(bp, c, Cp, vfrag);
+    input_tile_rows(
+        [&](int i, int j) {
+            const unsigned pair = d4[i][j >> 1];
+            const unsigned short bits = (unsigned short)((j & 1) ? (pair >> 16) : (pair & 0xffffu));
+            return (float)__builtin_bit_cast(_Float16, bits);
+        },
+        [&](int r, int s2, float v) {
+            const int p = r * 8 + s2;
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, to_f16(v)), vrs,
+                                                  voff, (int)(2 * p * pstride), kStream ? kNt : 0);
+        });
+}
+
+static hipError_t launch_input_run(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
+                                   int pad, int nh, int nw, int ldv, int64_t pstride,
+                                   hipStream_t s, bool stream_v, int vfrag) {
+    const int P = nh * nw;
+    const int64_t BP = (int64_t)B * P;
+    const int ncg = (ldv + 15) / 16;
+    const int64_t nblocks = ((BP + 15) / 16) * ncg;
+    if (nblocks >= ((int64_t)1 << 31) || BP >= ((int64_t)1 << 31) || pad > 4)
+        return hipErrorInvalidConfiguration;
+    const uintptr_t xp = reinterpret_cast<uintptr_t>(x);
+    const int xd = (int)(xp & 15);
+    const int64_t x_bytes = dword_ceil(2 * (int64_t)B * C * H * W + xd);
+    if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
+    const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
+    auto go = [&](auto kernel) {
+        launch(kernel, dim3((unsigned)nblocks), dim3(256), s, xa, reinterpret_cast<_Float16*>(V),
+               C, ldv, H, W, pad, nw, P, (int)BP, ncg, vfrag, pstride, (int)x_bytes, xd,
+               2 * 64 * pstride);
+    };
+    if (stream_v)
+        go(input_run_kernel<true>);
+    else
+        go(input_run_kernel<false>);
+    return hipGetLastError();
+}
+
 // Small problems (the tile-block grid under 256 workgroups, e.g. batch 1)
 // are latency-bound: they take the lane-parallel transforms, whose threads
 // run an eighth of the instruction chain. Large ones keep the tile-block
@@ -556,6 +691,18 @@ static bool latency_bound(int64_t rows, int n, int ch) { return widest_grid(rows
 hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                   int pad, int nh, int nw, int ldv, int64_t pstride,
                                   hipStream_t s, bool nhwc, bool stream_v, int vfrag) {
+    // The two-pass block layout from the run form when its grid fills the
+    // CUs (whole forwards in a graph, us, tile-block vs run form: conv3_x
+    // batch 32 24.25 vs 23.41 (input transform 8.78 vs 7.77), batch 24 22.75
+    // vs 21.94; 96@28^2 batch 32 19.91 vs 18.85; 48->40@13^2 batch 128 17.09
+    // vs 15.92; 128->256@14^2 batch 32 (144 workgroups) 21.18 vs 21.03; with
+    // few workgroups it loses: 128@28^2 batch 3 (40) 17.49 vs 18.44). Its V
+    // stays in the L2 for the products kernel (the workgroups of a tile
+    // block sit on the same XCD in both grids): streamed past it, the input
+    // transform ran 1 us faster but the products 1.4 us slower.
+    if (!nhwc && vfrag > 0 && pad <= 4 &&
+        ((int64_t)B * nh * nw + 15) / 16 * ((ldv + 15) / 16) >= 256)
+        return launch_input_run(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, false, vfrag);
     if (latency_bound((int64_t)B * nh, nw, ldv) ||
         (nhwc && (C % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0)))
         return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, nhwc, vfrag);

@@ -1,8 +1,8 @@
 """Input alignment and size do not change the output.
 
-The kernels that read x with 4- and 16-byte loads (the tile-block input
-transform of the three- and two-pass paths, the fused position-row kernel,
-both forms of the fused tile-block kernel) address it from a 16-byte
+The kernels that read x with 4- and 16-byte loads (the tile-block and run
+input transforms of the three- and two-pass paths, the fused position-row
+kernel, both forms of the fused tile-block kernel) address it from a 16-byte
 boundary through a buffer resource whose size must cover the dword that
 holds x's last element: a load returns zero for a dword that extends past
 the size. Each case runs the same input from several offsets (x_bytes 0, 2
@@ -25,6 +25,9 @@ CASES = [
     (25, 33, 40, 27, 27, 1),   # odd element count, tile-block input transform
     (1, 3, 5, 13, 13, 1),      # odd element count, small
     (3, 24, 16, 30, 30, 2),    # pad 2
+    (33, 65, 48, 27, 27, 1),   # two-pass: the run-form input transform (260 workgroups),
+                               # odd element count
+    (48, 64, 48, 28, 28, 2),   # the run form with pad 2
 ]
 OFFSETS = [0, 1, 2, 5, 7]  # halves past a 256-byte boundary
 
