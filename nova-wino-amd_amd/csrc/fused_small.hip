@@ -163,6 +163,7 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     if (tid < 2) *reinterpret_cast<unsigned long long*>(vs + kVHalves + 4 * tid) = 0ull;
 
     // ---- 2. input transform, kPpr patches per round (chains of input_lp_kernel) ----
+    const float one = opaque_one();
 #pragma unroll
     for (int rd = 0; rd < kRounds; rd++) {
         const int pc = rd * kPpr + (tid >> 3);
@@ -173,7 +174,8 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], d[rd][i], acc);
+                if (kBh[i][r] != 0.0f)
+                    acc = __builtin_fmaf(mix_coef(kBh[i][r], one), d[rd][i], acc);
             tp[r * 8 + j] = acc;
         }
         __syncthreads();
@@ -243,7 +245,8 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
             float s0 = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (kAh[r][i] != 0.0f) s0 = __builtin_fmaf(kAh[r][i], m8[i], s0);
+                if (kAh[r][i] != 0.0f)
+                    s0 = __builtin_fmaf(mix_coef(kAh[r][i], one), m8[i], s0);
             tp[r * 8 + j] = s0;
         }
         __syncthreads();

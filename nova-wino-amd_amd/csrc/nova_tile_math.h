@@ -103,10 +103,28 @@ __device__ __forceinline__ int xcd_remap(int L, int N) {
     return start + slot;
 }
 
+// An SGPR holding 1.0 that the optimizer cannot see through. A first-pass
+// term multiplies a table coefficient by an fp16 value widened to fp32; with a
+// coefficient of +-1 the compiler folds fma(c, x, acc) into acc +- x, which
+// needs x converted to fp32 by an instruction of its own, while fma(c, x, acc)
+// is one v_fma_mix_f32 that reads the fp16 operand in place. Both round once,
+// to the same value.
+__device__ __forceinline__ float opaque_one() {
+    float one = 1.0f;
+    asm("" : "+s"(one));
+    return one;
+}
+
+// Table coefficient c of a first-pass fma (see opaque_one).
+__device__ __forceinline__ float mix_coef(float c, float one) {
+    return c == 1.0f ? one : c == -1.0f ? -one : c;
+}
+
 // Input tile: ld(i, j) returns d[i][j] as fp32. Processes one input column j
 // at a time, which keeps every v[r][s] chain in j order.
 template <typename Load>
 __device__ __forceinline__ void input_tile(Load ld, float v[8][8]) {
+    const float one = opaque_one();
 #pragma unroll
     for (int r = 0; r < 8; r++)
 #pragma unroll
@@ -122,7 +140,8 @@ __device__ __forceinline__ void input_tile(Load ld, float v[8][8]) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], d[i], acc);
+                if (kBh[i][r] != 0.0f)
+                    acc = __builtin_fmaf(mix_coef(kBh[i][r], one), d[i], acc);
             t[r] = acc;
         }
 #pragma unroll
@@ -139,6 +158,7 @@ __device__ __forceinline__ void input_tile(Load ld, float v[8][8]) {
 // st(r, s, v) consumes each V value.
 template <typename Load, typename Store>
 __device__ __forceinline__ void input_tile_rows(Load ld, Store st) {
+    const float one = opaque_one();
 #pragma unroll
     for (int r = 0; r < 8; r++) {
         float t[8];
@@ -147,7 +167,8 @@ __device__ __forceinline__ void input_tile_rows(Load ld, Store st) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], ld(i, j), acc);
+                if (kBh[i][r] != 0.0f)
+                    acc = __builtin_fmaf(mix_coef(kBh[i][r], one), ld(i, j), acc);
             t[j] = acc;
         }
 #pragma unroll
@@ -166,13 +187,15 @@ __device__ __forceinline__ void input_tile_rows(Load ld, Store st) {
 // v[I][s] over j ascending. Only the input rows i with B[i][I] != 0 are read.
 template <int I, typename Load>
 __device__ __forceinline__ void input_row(Load ld, float out[8]) {
+    const float one = opaque_one();
     float t[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            if (kBh[i][I] != 0.0f) acc = __builtin_fmaf(kBh[i][I], ld(i, j), acc);
+            if (kBh[i][I] != 0.0f)
+                acc = __builtin_fmaf(mix_coef(kBh[i][I], one), ld(i, j), acc);
         t[j] = acc;
     }
 #pragma unroll
@@ -190,13 +213,15 @@ __device__ __forceinline__ void input_row(Load ld, float out[8]) {
 // starts at +0), so ld(i, j) may return anything for such a column.
 template <int I, typename Load>
 __device__ __forceinline__ void input_row_masked(Load ld, unsigned cols, float out[8]) {
+    const float one = opaque_one();
     float t[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            if (kBh[i][I] != 0.0f) acc = __builtin_fmaf(kBh[i][I], ld(i, j), acc);
+            if (kBh[i][I] != 0.0f)
+                acc = __builtin_fmaf(mix_coef(kBh[i][I], one), ld(i, j), acc);
         t[j] = ((cols >> j) & 1u) ? acc : 0.0f;
     }
 #pragma unroll
@@ -215,6 +240,7 @@ constexpr bool input_row_uses(int I, int i) { return kBh[i][I] != 0.0f; }
 // Output tile: ld(i, j) returns m[i][j] (position 8*i+j) as fp32.
 template <typename Load>
 __device__ __forceinline__ void output_tile(Load ld, float y[6][6]) {
+    const float one = opaque_one();
 #pragma unroll
     for (int r = 0; r < 6; r++)
 #pragma unroll
@@ -230,7 +256,8 @@ __device__ __forceinline__ void output_tile(Load ld, float y[6][6]) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (kAh[r][i] != 0.0f) acc = __builtin_fmaf(kAh[r][i], m[i], acc);
+                if (kAh[r][i] != 0.0f)
+                    acc = __builtin_fmaf(mix_coef(kAh[r][i], one), m[i], acc);
             t[r] = acc;
         }
 #pragma unroll

@@ -469,13 +469,14 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
         d[i] = (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
                                                        xrs, off, 0, 0));
     }
+    const float one = opaque_one();
     float* tp = tls + (wv * 8 + cl) * kLpPitch;
 #pragma unroll
     for (int r = 0; r < 8; r++) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(kBh[i][r], d[i], acc);
+            if (kBh[i][r] != 0.0f) acc = __builtin_fmaf(mix_coef(kBh[i][r], one), d[i], acc);
         tp[r * 8 + j] = acc;
     }
     __syncthreads();
@@ -1007,13 +1008,14 @@ __global__ __launch_bounds__(256) void output_lp_kernel(
     for (int i = 0; i < 8; i++)
         m[i] = (float)__builtin_bit_cast(
             _Float16, __builtin_amdgcn_raw_buffer_load_b16(mrs, moff, (int)(16 * i * pstride), 0));
+    const float one = opaque_one();
     float* tp = tls + (wv * 8 + kl) * kLpPitch;
 #pragma unroll
     for (int r = 0; r < 6; r++) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            if (kAh[r][i] != 0.0f) acc = __builtin_fmaf(kAh[r][i], m[i], acc);
+            if (kAh[r][i] != 0.0f) acc = __builtin_fmaf(mix_coef(kAh[r][i], one), m[i], acc);
         tp[r * 8 + j] = acc;
     }
     __syncthreads();
