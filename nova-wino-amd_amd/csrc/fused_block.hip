@@ -696,13 +696,10 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
                     const auto sw = __builtin_amdgcn_permlane16_swap(
                         __builtin_bit_cast(unsigned, pend), __builtin_bit_cast(unsigned, v), false,
                         false);
-                    const unsigned lo = __builtin_bit_cast(
-                        uint16_t, to_f16(__builtin_bit_cast(float, (unsigned)sw[0])));
-                    const unsigned hi = __builtin_bit_cast(
-                        uint16_t, to_f16(__builtin_bit_cast(float, (unsigned)sw[1])));
                     const int pos = r * 8 + s2 - 1 + (ct & 1);
-                    *reinterpret_cast<unsigned*>(vj + pos * (NS * 512) +
-                                                 v_index_sw(0, ct & ~1, t)) = lo | (hi << 16);
+                    *reinterpret_cast<unsigned*>(vj + pos * (NS * 512) + v_index_sw(0, ct & ~1, t)) =
+                        pack_f16x2(__builtin_bit_cast(float, (unsigned)sw[0]),
+                                   __builtin_bit_cast(float, (unsigned)sw[1]));
                 }
             });
     }

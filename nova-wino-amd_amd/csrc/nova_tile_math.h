@@ -26,6 +26,17 @@ __device__ __forceinline__ _Float16 to_f16(float v) {
     return (_Float16)v;
 }
 
+// Two fp32 values rounded to fp16 (nearest even) and packed, lo in the low
+// half: one v_cvt_pk_f16_f32, the same bits as two to_f16 calls (the empty
+// asm keeps each value a separate fp32 rounding, as in to_f16).
+__device__ __forceinline__ unsigned pack_f16x2(float lo, float hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    asm("" : "+v"(lo));
+    asm("" : "+v"(hi));
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(f2{lo, hi}, h2));
+}
+
 // Output epilogue for channel k: the convolution value rounded to fp16, then
 // the reference's separate bias add (`y + bias.half()`: fp16 + fp16 summed in
 // fp32, rounded once) and an optional ReLU (negative values -> 0). bias is a
