@@ -121,7 +121,7 @@ def test_window_bytes_validation():
     try:
         lib.nova_set_window_bytes(h, -1)
         assert lib.nova_get_last_error() != 0
-        lib.nova_set_path(h, 7)
+        lib.nova_set_path(h, 8)  # paths are 0..7
         assert lib.nova_get_last_error() != 0
         lib.nova_set_path(h, 4)
         assert lib.nova_get_last_error() == 0
