@@ -67,6 +67,7 @@ struct FusedArgs {
     const _Float16* bias;  // output epilogue (null: none)
     int relu;
     const _Float16* residual;  // added after the bias, y's layout (null: none)
+    int nwg;                   // workgroups in the grid (gridDim.x; a kernel that reads gridDim gets hidden arguments)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(kFThreads, 1) void fused_kernel(FusedArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // ---- which (image, tile block, channel block, position row) ----
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, a.nwg);
     const int i = L & 7;
     const int blk = L >> 3;  // ((b*nbh + bh)*nbw + bw)*n_kb + kb
     int r = blk;
@@ -493,6 +494,7 @@ hipError_t launch_fused(const uint16_t* x, const uint16_t* Uf, uint16_t* y, uint
     a.nkt = (K + 15) / 16;
     a.nkp = (Cp + 31) / 32;
     const dim3 grid((unsigned)p.grid), block(kFThreads);
+    a.nwg = (int)grid.x;
     switch (p.nm) {
         case 1: launch(fused_kernel<1>, grid, block, s, a); break;
         case 2: launch(fused_kernel<2>, grid, block, s, a); break;

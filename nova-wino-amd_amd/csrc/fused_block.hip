@@ -77,6 +77,7 @@ struct BlockArgs {
     int relu;
     const _Float16* residual;  // added after the bias, y's layout (null: none)
     int cols;                  // NHWC: staged pixels per row (6*nw + 2)
+    int nwg;                   // workgroups in the grid (gridDim.x; a kernel that reads gridDim gets hidden arguments)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel(BlockArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = position row
 
     // ---- work item: (image b, 16-tile run, 64-channel output block) ----
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, a.nwg);
     const int kblk = L % a.n_kblk;
     const int rest = L / a.n_kblk;
     const int run = rest % a.nruns;
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(kBT, 1) void fused_block_kernel_direct(BlockArgs a)
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = position row
 
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, a.nwg);
     const int kblk = L % a.n_kblk;
     const int rest = L / a.n_kblk;
     const int run = rest % a.nruns;
@@ -836,6 +837,7 @@ hipError_t launch_fused_block(const uint16_t* x, const uint16_t* U, uint16_t* y,
                     : 0;
     a.cols = p.cols;
     const dim3 grid((unsigned)p.grid), block(kBT);
+    a.nwg = (int)grid.x;
     const bool epi = epilogue_needed(ep.bias, ep.relu, ep.residual);
     auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
     if (Cp <= 64) {

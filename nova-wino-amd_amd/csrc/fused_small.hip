@@ -58,6 +58,7 @@ struct SmallArgs {
     int nkb;       // 16-channel output blocks
     int nkt, nkp;  // 16-row tiles and 32-channel chunks of the fragment-ordered U
     int y_pairs;   // 1: NCHW rows stored as 4-byte pairs (even Wo, 4-byte aligned y)
+    int nwg;       // workgroups in the grid (gridDim.x; a kernel that reads gridDim gets hidden arguments)
     const _Float16* bias;
     int relu;
     const _Float16* residual;
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(NTH, 1) void fused_small_kernel(SmallArgs a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int L = xcd_remap((int)blockIdx.x, a.nwg);
     const int kb = L % a.nkb;
     const int rest = L / a.nkb;
     const int tg = rest % a.ntg;
@@ -384,6 +385,7 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
     a.relu = ep.relu;
     a.residual = reinterpret_cast<const _Float16*>(ep.residual);
     const dim3 grid((unsigned)p.grid), block((unsigned)p.threads);
+    a.nwg = (int)grid.x;
     if ((p.tiles != 2 && (p.tiles != 4 || p.nkp != 2)) || (p.threads != 512 && p.threads != 1024) ||
         (p.nkp != 2 && p.nkp != 4) || (p.nkp == 4 && p.threads != 1024) || Cp > 32 * p.nkp)
         return hipErrorInvalidConfiguration;

@@ -51,6 +51,7 @@ struct GoArgs {
     int u_bytes, v_bytes, y_bytes;
     int K, Cp, BP, P, nw, Ho, Wo;
     int nkb;      // 32-channel output blocks
+    int nwg;      // workgroups in the grid (gridDim.x, passed to keep hidden arguments off)
     int nkt;      // 16-row tiles of U
     int nbb;      // 16-tile blocks of V
     int y_pairs;  // 1: NCHW rows stored as 4-byte pairs (even Wo, 4-byte aligned y)
@@ -74,7 +75,7 @@ void gemm_out_kernel(GoArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = position row
 
     // output block fastest: the workgroups of one tile block read its V in one L2
-    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int L = xcd_remap((int)blockIdx.x, a.nwg);
     const int kb32 = L % a.nkb;
     const int bp0 = (L / a.nkb) * kGoT;
     const int k0 = kb32 * kGoK;
@@ -277,6 +278,7 @@ hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, i
     a.relu = ep.relu;
     a.residual = reinterpret_cast<const _Float16*>(ep.residual);
     const dim3 g((unsigned)grid), blk(kGoThreads);
+    a.nwg = (int)g.x;
     auto go = [&](auto kernel) { launch(kernel, g, blk, s, a); };
     if (epilogue_needed(ep.bias, ep.relu, ep.residual))
         nhwc ? go(gemm_out_kernel<true, true>) : go(gemm_out_kernel<false, true>);

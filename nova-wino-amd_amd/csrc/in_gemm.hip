@@ -70,6 +70,7 @@ struct InGemmArgs {
     int nkt;       // 16-row output-channel tiles
     int nsteps;    // 32-channel steps (Cp / 32 rounded up)
     int vpitch;    // halves per (position, tile) row of V in LDS: Cp + 8
+    int nwg;       // workgroups in the grid (gridDim.x; a kernel that reads gridDim gets hidden arguments)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(kIT, 1) void in_gemm_kernel(InGemmArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // XCD-aware order: the tile groups of one (row, channel group) -- the
     // workgroups that read the same U blocks -- are neighbours
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, a.nwg);
     const int tg = L % a.ntg;
     const int rest = L / a.ntg;
     const int r = rest % 8;
@@ -471,6 +472,7 @@ hipError_t launch_in_gemm(const uint16_t* x, const uint16_t* Uw, uint16_t* M, in
     a.nsteps = p.nsteps;
     a.vpitch = Cp + 8;
     const dim3 grid((unsigned)p.grid), block(kIT);
+    a.nwg = (int)grid.x;
     auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
     auto pick = [&](auto nh_) {
         constexpr bool kN = decltype(nh_)::value;

@@ -35,6 +35,18 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t 
     }
 }
 
+// launch() for a kernel with a one-dimensional grid whose last parameter is
+// its number of workgroups (grid.x, appended here). Kernels take that count
+// as an argument instead of reading gridDim or blockDim: either read makes
+// the compiler add 256 bytes of hidden kernel arguments, which the runtime
+// writes to device memory on every launch -- 0.7-0.8 us of host time per
+// launch on MI355X (2.8 us per launch without them, 3.5 with).
+template <typename... KArgs, typename... Args>
+inline void launch_n(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+                     Args... args) {
+    launch(kernel, grid, block, s, args..., (int)grid.x);
+}
+
 // Error codes returned by nova_get_last_error().
 enum Status : int {
     kOk = 0,

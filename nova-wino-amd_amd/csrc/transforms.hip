@@ -26,7 +26,7 @@ template <bool kRefLayout, typename WT>
 __global__ __launch_bounds__(256) void filter_transform_kernel(const WT* __restrict__ w,
                                                                _Float16* __restrict__ U, int K,
                                                                int C, int Cp) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256-thread blocks
     const int cols = kRefLayout ? C : Cp;  // threads along c (product layout pads)
     if (idx >= (int64_t)K * cols) return;
     int k, c;
@@ -92,7 +92,7 @@ hipError_t launch_filter_transform_gemm(const void* w, bool w_f16, uint16_t* U, 
 __global__ __launch_bounds__(256) void u_frag_kernel(const _Float16* __restrict__ U,
                                                       _Float16* __restrict__ Uf, int K, int Cp,
                                                       int nkt, int nkp, int64_t nslots) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256-thread blocks
     if (i >= nslots) return;
     const int ks = (int)(i & 1);
     const int lane = (int)((i >> 1) & 63);
@@ -124,7 +124,7 @@ hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStre
 __global__ __launch_bounds__(256) void u_wfrag_kernel(const _Float16* __restrict__ U,
                                                        _Float16* __restrict__ Uw, int K, int Cp,
                                                        int nkt, int nkp, int64_t nslots) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 256-thread blocks
     if (i >= nslots) return;
     const int lane = (int)(i & 63);
     const int64_t frag = i >> 6;  // (p*nkt + kt)*nkp + j
@@ -265,12 +265,12 @@ template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int xd,
-    int64_t v_bytes, int vfrag) {
+    int64_t v_bytes, int vfrag, int nwg) {
     using G = InGeom<TW>;
     __shared__ __align__(16) unsigned char sx[G::kBytes];
     // 1-D grid over (tile block, tile row, image x channel block), x fastest
     const int nwb = (nw + TW - 1) / TW;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, nwg);
     const int tw0 = (L % nwb) * TW;
     const int th = (L / nwb) % nh;
     const int bz = L / (nwb * nh);
@@ -365,7 +365,7 @@ template <int TW, bool kStream>
 __global__ __launch_bounds__(256) void input_nhwc_kernel(
     const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int64_t v_bytes,
-    int vfrag) {
+    int vfrag, int nwg) {
     constexpr int kCB = 256 / TW;
     constexpr int kCols = 6 * TW + 2;
     constexpr int kPix = kCB + 8;            // halves per staged pixel
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256) void input_nhwc_kernel(
     constexpr int kRounds = (kUnits + 255) / 256;
     __shared__ __align__(16) _Float16 sx[8 * kCols * kPix];
     const int nwb = (nw + TW - 1) / TW;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, nwg);
     const int tw0 = (L % nwb) * TW;
     const int th = (L / nwb) % nh;
     const int bz = L / (nwb * nh);
@@ -441,12 +441,12 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
                                                        _Float16* __restrict__ V, int C, int H,
                                                        int W, int pad, int nh, int nw, int ldv,
                                                        int64_t pstride, int ncg, int x_bytes,
-                                                       int64_t v_bytes, int vfrag) {
+                                                       int64_t v_bytes, int vfrag, int nwg) {
     __shared__ float tls[4 * 8 * kLpPitch];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int j = lane & 7, cl = lane >> 3;
-    const int item = xcd_remap(blockIdx.x, gridDim.x);  // (tile bp, 32-channel group)
+    const int item = xcd_remap(blockIdx.x, nwg);  // (tile bp, 32-channel group)
     const int bp = item / ncg;
     const int c = (item - bp * ncg) * 32 + wv * 8 + cl;
     const int tw = bp % nw;
@@ -504,11 +504,11 @@ static hipError_t launch_input_lp(const uint16_t* x, uint16_t* V, int B, int C, 
     const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     if (nhwc)
-        launch(input_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
+        launch_n(input_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
             nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
     else
-        launch(input_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
+        launch_n(input_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
             reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
             nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
     return hipGetLastError();
@@ -559,10 +559,10 @@ template <bool kStream>
 __global__ __launch_bounds__(256) void input_run_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int Cp, int H, int W,
     int pad, int nw, int P, int BP, int ncg, int vfrag, int64_t pstride, int x_bytes, int xd,
-    int64_t v_bytes) {
+    int64_t v_bytes, int nwg) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, nwg);
     const int cg = L % ncg, blk = L / ncg;
     const int c = cg * 16 + 8 * (wave >> 1) + (lane & 7);
     const int t = 8 * (wave & 1) + (lane >> 3);
@@ -662,7 +662,7 @@ static hipError_t launch_input_run(const uint16_t* x, uint16_t* V, int B, int C,
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
     auto go = [&](auto kernel) {
-        launch(kernel, dim3((unsigned)nblocks), dim3(256), s, xa, reinterpret_cast<_Float16*>(V),
+        launch_n(kernel, dim3((unsigned)nblocks), dim3(256), s, xa, reinterpret_cast<_Float16*>(V),
                C, ldv, H, W, pad, nw, P, (int)BP, ncg, vfrag, pstride, (int)x_bytes, xd,
                2 * 64 * pstride);
     };
@@ -719,7 +719,7 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
         if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
         const _Float16* xh = reinterpret_cast<const _Float16*>(x);
         auto go = [&](auto kernel) {
-            launch(kernel, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
+            launch_n(kernel, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
                    (int)x_bytes, 2 * 64 * pstride, vfrag);
         };
         if (tw == 2)
@@ -738,7 +738,7 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
     auto go = [&](auto kernel) {
-        launch(kernel, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
+        launch_n(kernel, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
                (int)x_bytes, xd, 2 * 64 * pstride, vfrag);
     };
     if (tw == 2)
@@ -776,12 +776,12 @@ template <int TW, int kVW, bool kEpi>
 __global__ __launch_bounds__(256) void output_transform_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
-    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
+    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res, int nwg) {
     using G = OutGeom<TW>;
     constexpr int kPlane = G::template plane<kVW>();
     __shared__ __align__(16) _Float16 sy[G::kKB * kPlane];
     const int nwb = (nw + TW - 1) / TW;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, nwg);
     const int tw0 = (L % nwb) * TW;
     const int th = (L / nwb) % nh;
     const int bz = L / (nwb * nh);
@@ -900,10 +900,10 @@ template <int TW, bool kEpi>
 __global__ __launch_bounds__(256) void output_nhwc_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int kblocks, int64_t m_bytes, int64_t y_bytes,
-    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
+    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res, int nwg) {
     constexpr int kKB = 256 / TW;
     const int nwb = (nw + TW - 1) / TW;
-    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int L = xcd_remap(blockIdx.x, nwg);
     const int tw0 = (L % nwb) * TW;
     const int th = (L / nwb) % nh;
     const int bz = L / (nwb * nh);
@@ -953,7 +953,7 @@ static void launch_out_tw(int vw, bool epi, dim3 grid, hipStream_t s, const _Flo
                           const _Float16* bias, int relu, const _Float16* res) {
     const dim3 block(256);
     auto go = [&](auto kernel) {
-        launch(kernel, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes,
+        launch_n(kernel, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks, m_bytes,
                y_bytes, bias, relu, res);
     };
     if (epi) {
@@ -988,12 +988,12 @@ template <bool kNhwc, bool kEpi>
 __global__ __launch_bounds__(256) void output_lp_kernel(
     const _Float16* __restrict__ M, _Float16* __restrict__ y, int K, int Ho, int Wo, int nh,
     int nw, int ldm, int64_t pstride, int nkg, int64_t m_bytes, int64_t y_bytes, int pairs,
-    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res) {
+    const _Float16* __restrict__ bias, int relu, const _Float16* __restrict__ res, int nwg) {
     __shared__ float tls[4 * 8 * kLpPitch];
     const int lane = threadIdx.x & 63;
     const int wv = threadIdx.x >> 6;
     const int j = lane & 7, kl = lane >> 3;
-    const int item = xcd_remap(blockIdx.x, gridDim.x);  // (tile bp, 32-channel group)
+    const int item = xcd_remap(blockIdx.x, nwg);  // (tile bp, 32-channel group)
     const int bp = item / nkg;
     const int k = (item - bp * nkg) * 32 + wv * 8 + kl;
     const int tw = bp % nw;
@@ -1103,7 +1103,7 @@ static hipError_t launch_output_lp(const uint16_t* M, uint16_t* y, int B, int K,
                           ? 1
                           : 0;
     auto go = [&](auto kernel) {
-        launch(kernel, dim3((unsigned)items), dim3(256), s, reinterpret_cast<const _Float16*>(M),
+        launch_n(kernel, dim3((unsigned)items), dim3(256), s, reinterpret_cast<const _Float16*>(M),
                reinterpret_cast<_Float16*>(y), K, Ho, Wo, nh, nw, ldm, pstride, nkg,
                2 * 64 * pstride, y_bytes, pairs, reinterpret_cast<const _Float16*>(ep.bias),
                ep.relu, reinterpret_cast<const _Float16*>(ep.residual));
@@ -1142,7 +1142,7 @@ hipError_t launch_output_transform(const uint16_t* M, uint16_t* y, int B, int K,
         const _Float16* res = reinterpret_cast<const _Float16*>(ep.residual);
         const dim3 grid((unsigned)nblocks), block(256);
         auto go = [&](auto kernel) {
-            launch(kernel, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
+            launch_n(kernel, grid, block, s, Mh, yh, K, Ho, Wo, nh, nw, ldm, pstride, kblocks,
                    2 * 64 * pstride, y_bytes, bias, ep.relu, res);
         };
         const bool epi = epilogue_needed(bias, ep.relu, res);

@@ -156,7 +156,7 @@ template <int TK, int TB, int WK, int WB, int PF, int SM>
 __global__ __launch_bounds__(64 * WK * WB) void wgemm_lds_kernel(const _Float16* __restrict__ U,
                                                         const _Float16* __restrict__ V,
                                                         _Float16* __restrict__ M, int K, int Cp,
-                                                        int BP) {
+                                                        int BP, int nwg) {
     constexpr int kThreads = 64 * WK * WB;
     constexpr int MT = TK / WK / 16;  // 16x16 tiles per wave along k
     constexpr int NT = TB / WB / 16;  // along bp
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(64 * WK * WB) void wgemm_lds_kernel(const _Float16*
     // (position, k-tile, bp-tile) items with the bp tile fastest, so all
     // tiles of a position meet in one L2 and U_p, V_p leave HBM once.
     const int nbt = (BP + TB - 1) / TB, nkt = (K + TK - 1) / TK;
-    const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int item = xcd_remap((int)blockIdx.x, nwg);
     const int p = item / (nbt * nkt);
     const int rem = item - p * (nbt * nkt);
     const int k0 = (rem / nbt) * TK;
@@ -361,7 +361,7 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
                              int BP, hipStream_t s) {
     const unsigned grid = 64u * (unsigned)((BP + TB - 1) / TB) * (unsigned)((K + TK - 1) / TK);
     auto go = [&](auto kernel) {
-        launch(kernel, dim3(grid), dim3(64 * WK * WB), s, reinterpret_cast<const _Float16*>(U),
+        launch_n(kernel, dim3(grid), dim3(64 * WK * WB), s, reinterpret_cast<const _Float16*>(U),
                reinterpret_cast<const _Float16*>(V), reinterpret_cast<_Float16*>(M), K, Cp, BP);
     };
     if (m_epilogue(K, BP) == 2)
@@ -396,13 +396,13 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 template <int MT, int NT, int PD, int WPB>
 __global__ __launch_bounds__(64 * WPB) void wgemm_block_kernel(
     const _Float16* __restrict__ Uw, const _Float16* __restrict__ Vb, _Float16* __restrict__ M,
-    int K, int Cp, int BP, int u_bytes, int v_bytes, int m_bytes) {
+    int K, int Cp, int BP, int u_bytes, int v_bytes, int m_bytes, int nwg) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int nkt = (K + 15) / 16;
     const int nkg = (nkt + MT - 1) / MT;
     // XCD-aware: each XCD takes a contiguous run of positions
-    const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x) * WPB + wave;
+    const int item = xcd_remap((int)blockIdx.x, nwg) * WPB + wave;
     if (item >= 64 * nkg) return;  // no barrier below: idle waves may leave
     const int p = item / nkg;
     const int kt0 = (item - p * nkg) * MT;
@@ -491,7 +491,7 @@ hipError_t launch_wgemm_blocks(const uint16_t* Uw, const uint16_t* Vb, uint16_t*
     const int nkg = ((K + 15) / 16 + kMT - 1) / kMT;
     const unsigned grid = (unsigned)((64 * nkg + kWPB - 1) / kWPB);
     auto go = [&](auto kernel) {
-        launch(kernel, dim3(grid), dim3(64 * kWPB), s, reinterpret_cast<const _Float16*>(Uw),
+        launch_n(kernel, dim3(grid), dim3(64 * kWPB), s, reinterpret_cast<const _Float16*>(Uw),
                reinterpret_cast<const _Float16*>(Vb), reinterpret_cast<_Float16*>(M), K, Cp, BP,
                (int)(2 * u_frag_elems(K, Cp)), (int)(2 * gemm_out_v_elems(Cp, BP)),
                (int)(2 * (int64_t)64 * BP * K));

@@ -195,12 +195,12 @@ constexpr int kAhead = 2;
 
 __global__ __launch_bounds__(kWgThreads, 1) void wg_gemm_proj_kernel(
     const float* __restrict__ Mt, const float* __restrict__ Vt, float* __restrict__ out, int K,
-    int C, int BPp, int chunk, int nsplit, int accumulate) {
+    int C, int BPp, int chunk, int nsplit, int accumulate, int nwg) {
     __shared__ float red[4][144][64];  // 144 KB: every wave's accumulators
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int ntk = (K + kProjK - 1) / kProjK, ntc = (C + kProjC - 1) / kProjC;
-    const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int L = xcd_remap((int)blockIdx.x, nwg);
     const int tile = L % (ntk * ntc), sp = L / (ntk * ntc);
     const int k0 = (tile % ntk) * kProjK, c0 = (tile / ntk) * kProjC;
     const int r16 = lane & 15, g = lane >> 4;
@@ -409,7 +409,7 @@ hipError_t launch_wgrad(const uint16_t* x, const void* dy, bool dy_f32, float* d
         const int chunk = 16 * ((steps + pl.nsplit - 1) / pl.nsplit);
         const int64_t grid = (int64_t)pl.nsplit * ((K + kProjK - 1) / kProjK) *
                              ((C + kProjC - 1) / kProjC);
-        launch(wg_gemm_proj_kernel, dim3((unsigned)grid), dim3(kWgThreads), s,
+        launch_n(wg_gemm_proj_kernel, dim3((unsigned)grid), dim3(kWgThreads), s,
                static_cast<const float*>(Mt), static_cast<const float*>(Vt), part, K, C, BPp,
                chunk, pl.nsplit, b0 > 0 ? 1 : 0);
         const hipError_t e = hipGetLastError();
