@@ -80,6 +80,44 @@ def test_cached_forward_invalidation():
     torch.cuda.synchronize()
 
 
+def test_cached_forward_bias_changes_and_fresh_outputs():
+    """The cached path reads the parameters from the module's parameter
+    table: an in-place bias update, a bias set to None and a removed bias
+    entry are all seen; and the output it allocates (like the input when the
+    shapes agree) is a new tensor at every call."""
+    from nova_winograd import NovaWinogradConv2d
+
+    print("[module cache: bias, outputs]", flush=True)
+    torch.manual_seed(12)
+    conv = NovaWinogradConv2d(32, 32, kernel_size=3, padding=1, bias=True).to(DEV)
+    with torch.no_grad():
+        conv.bias.copy_(torch.randn(32))
+    x = torch.randn(2, 32, 14, 14, device=DEV).half()
+    with torch.no_grad():
+        ya = conv(x)
+        yb = conv(x)  # cached path, output allocated like x
+        assert conv._state is not None
+        assert yb.shape == x.shape and yb.dtype == torch.float16 and yb.is_contiguous()
+        assert ya.data_ptr() != yb.data_ptr() and yb.data_ptr() != x.data_ptr()
+        assert torch.equal(ya, yb)
+
+        conv.bias.add_(0.25)  # in place: the bias version changes
+        yc = conv(x)
+        assert torch.equal(yc, _fresh(conv)(x))
+        assert not torch.equal(yc, yb)
+
+        conv.bias = None  # the entry stays, holding None
+        yd = conv(x)
+        assert torch.equal(yd, _fresh(conv)(x))
+        ye = conv(x)  # cached path without a bias
+        assert torch.equal(ye, yd)
+
+        del conv.bias  # no entry at all: the full path, as nn.Conv2d would fail
+        with pytest.raises(AttributeError):
+            conv(x)
+    torch.cuda.synchronize()
+
+
 def test_functional_cached_handle(monkeypatch):
     """nova_forward runs on the persistent per-device handle: the filter is
     transformed once for repeated calls with the same weight, again after an
