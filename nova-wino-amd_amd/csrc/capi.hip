@@ -394,13 +394,19 @@ bool two_pass_possible(int C, int K) { return C <= 128 && K <= 256 && 2 * K >= C
 // 26.7 vs 22.4; 96->256@14^2 B=32 23.1 vs 16.8; 64->256@28^2 B=16 25.0 vs
 // 16.8, B=20 28.2 vs 18.2; 128->192@14^2 B=48 26.1 vs 21.5): each two-pass
 // workgroup reads all Cp channels of its operands, so its time follows Cp,
-// not K.
+// not K. Grids of at most one 16-channel workgroup per CU run 16 output
+// channels per workgroup, two per CU (gemm_out_kb); at most 128 output
+// channels that admits grids of 64 such workgroups (us, three-pass vs
+// two-pass: 96@28^2 B=8, 78 workgroups, 14.10 vs 13.76; 128@28^2 B=8, 104:
+// 16.33 vs 15.95; 128@28^2 B=4, 56: 11.69 vs 14.74 stays three-pass).
 bool two_pass_wins(const Handle* Hd, const Shape& s) {
     if (!two_pass_possible(Hd->C, Hd->K)) return false;
-    const int64_t grid = gemm_out_grid(Hd->K, (int)std::min<int64_t>(s.BP, INT32_MAX));
+    const int bp = (int)std::min<int64_t>(s.BP, INT32_MAX);
+    const int64_t grid = gemm_out_grid(Hd->K, bp);
     const int64_t v_bytes = 2 * gemm_out_v_elems(Hd->Cp, s.BP);
-    const int64_t min_grid = Hd->K > 128 ? 128 : 64;
-    return grid >= min_grid && grid <= Hd->cus && v_bytes <= (int64_t)20 << 20;
+    if (grid > Hd->cus || v_bytes > (int64_t)20 << 20) return false;
+    if (Hd->K > 128) return grid >= 128;
+    return gemm_out_grid(Hd->K, bp, gemm_out_kb(Hd->K, bp, Hd->cus)) >= 64;
 }
 
 bool in_gemm_plan_for(const Handle* Hd, const Shape& s, InGemmPlan* p) {
@@ -472,11 +478,17 @@ int choose_path(const Handle* Hd, const Shape& s) {
     // 64@112^2 B=1 14.9 vs 13.3; 48@112^2 B=1 14.1 vs 12.4; 48->40@13^2 B=64
     // 15.1 vs 14.2; 32@56^2 B=4 11.0 vs 8.5, B=8 11.7 (fused tile-block) vs
     // 13.6; 32@112^2 B=2 11.7 vs 12.2; beyond four per CU it loses (64@112^2
-    // B=2 16.2 vs 21.4; 48->40@13^2 B=128 16.9 vs 24.4).
+    // B=2 16.2 vs 21.4; 48->40@13^2 B=128 16.9 vs 24.4). Where the two-pass
+    // path can run, it takes over above two and a half small-problem
+    // workgroups per CU (us, small kernel vs two-pass at 16 channels per
+    // workgroup: 64@56^2 B=3, 2.3 per CU, 12.21 vs 12.62; B=4, 3.1: 14.51 vs
+    // 12.80; B=5 15.14 vs 13.02; 64@28^2 B=16, 3.1: 13.71 vs 12.64; 48->40@13^2
+    // B=64, 3.4: 14.01 vs 13.13; 48@56^2 B=4, 2.3: 11.88 vs 12.48).
     FusedSmallPlan sp;
-    if (Hd->C <= 64 && Hd->K <= 64 && fused_small_plan_for(Hd, s, &sp) &&
-        sp.grid <= (Hd->Cp > 32 ? 4 : 2) * (int64_t)Hd->cus)
-        return 5;
+    if (Hd->C <= 64 && Hd->K <= 64 && fused_small_plan_for(Hd, s, &sp)) {
+        const int64_t cap2 = Hd->Cp <= 32 ? 4 : two_pass_wins(Hd, s) ? 5 : 8;  // 2 x per CU
+        if (2 * sp.grid <= cap2 * (int64_t)Hd->cus) return 5;
+    }
     FusedBlockPlan bp;
     if (Hd->C <= 64 && Hd->K <= 64 && fused_block_plan_for(Hd, s, &bp)) {
         const int64_t waves = (bp.grid + Hd->cus - 1) / Hd->cus;
@@ -597,8 +609,9 @@ bool run_two_pass(Handle* Hd, const uint16_t* x, uint16_t* y, const Shape& s, ui
         return launch_input_transform(x, V, s.B, C, s.H, s.W, s.pad, s.nh, s.nw, Cp, pstride, st,
                                       nhwc, stream_v, vfrag);
     };
+    const int go_kb = gemm_out_kb(K, (int)s.BP, Hd->cus);
     auto go = [=]() {
-        return launch_gemm_out(U, V, y, s.B, K, Cp, s.nh, s.nw, s.Ho, s.Wo, st, ep, nhwc);
+        return launch_gemm_out(U, V, y, s.B, K, Cp, s.nh, s.nw, s.Ho, s.Wo, st, ep, nhwc, go_kb);
     };
     if (remember) {
         pf.last[kKindInput] = in;

@@ -6,7 +6,10 @@
 // Workgroup = 16 consecutive tiles (bp, across images) x 32 output channels x
 // all 64 positions; 512 threads, wave w owns position row w (8 positions) and
 // keeps 8 x 2 fp32 16x16 accumulators (64 registers) for the whole channel
-// loop. Per 32-channel step a lane loads its operands with the three-pass
+// loop. Grids that would leave CUs idle at 32 channels (at most one
+// 16-channel workgroup per CU) take 16 output channels per workgroup and run
+// two workgroups per CU instead (8 x 1 accumulators, one step of operands in
+// flight per wave, the other workgroup's waves covering its loads). Per 32-channel step a lane loads its operands with the three-pass
 // GEMM's lane layout -- A = U_p rows (16 k x 32 c), B = V_p rows (32 c x 16
 // bp), lane l holding row l % 16 and channels 8*(l/16) .. +7 -- from copies
 // in which that is contiguous (U: launch_u_wfrag blocks; V: the input
@@ -37,12 +40,17 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGoT = 16;        // tiles per workgroup
-constexpr int kGoK = 32;        // output channels per workgroup
 constexpr int kGoThreads = 512;  // 8 waves: one per position row
 constexpr int kGoPitch = 72;    // halves per (k, tile) row of M: 64 positions + 8
-constexpr int kGoTileP = kGoK * kGoPitch + 8;  // channels-last: halves per tile
-constexpr int kGoMsHalves = kGoT * kGoTileP;   // >= kGoK * kGoT * kGoPitch
 constexpr int kGoOob = (int)0x80000000;
+// Output channels per workgroup: KB 16-row tiles of U (KB = 2: 32 channels,
+// one workgroup per CU; KB = 1: 16, two per CU)
+template <int KB>
+struct GoGeom {
+    static constexpr int kK = 16 * KB;
+    static constexpr int kTileP = kK * kGoPitch + 8;  // channels-last: halves per tile
+    static constexpr int kMsHalves = kGoT * kTileP;   // >= kK * kGoT * kGoPitch
+};
 
 struct GoArgs {
     const _Float16* U;  // U blocks [64][nkt][Cp/32][lane][8]
@@ -50,7 +58,7 @@ struct GoArgs {
     _Float16* y;
     int u_bytes, v_bytes, y_bytes;
     int K, Cp, BP, P, nw, Ho, Wo;
-    int nkb;      // 32-channel output blocks
+    int nkb;      // output-channel blocks (16 * KB channels each)
     int nwg;      // workgroups in the grid (gridDim.x, passed to keep hidden arguments off)
     int nkt;      // 16-row tiles of U
     int nbb;      // 16-tile blocks of V
@@ -64,21 +72,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t go_rsrc(const void* p, int byt
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 
-// Two waves per SIMD (one workgroup per CU): up to 256 registers per lane,
-// room for two steps of operands beside the accumulators.
-template <bool kNhwc, bool kEpi>
-__global__ __launch_bounds__(kGoThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// KB = 2: one workgroup per CU, two waves per SIMD, up to 256 registers per
+// lane, room for two steps of operands beside the accumulators (double
+// buffer). KB = 1: two workgroups per CU, four waves per SIMD, at most 128
+// registers, one step of operands (measured on MI355X, graph of ten forwards,
+// us, one vs two workgroups per CU at 16 channels: 64@56^2 B=4 13.23 vs
+// 12.80, B=8 14.25 vs 13.76; 128@28^2 B=8 16.19 vs 15.95; 96@28^2 B=8 13.76
+// vs 13.90).
+template <int KB, bool kNhwc, bool kEpi>
+__global__ __launch_bounds__(kGoThreads) __attribute__((amdgpu_waves_per_eu(6 - 2 * KB, 6 - 2 * KB)))
 void gemm_out_kernel(GoArgs a) {
-    __shared__ __align__(16) _Float16 ms[kGoMsHalves];
+    static_assert(KB == 1 || KB == 2, "16 or 32 output channels per workgroup");
+    using G = GoGeom<KB>;
+    __shared__ __align__(16) _Float16 ms[G::kMsHalves];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // = position row
 
     // output block fastest: the workgroups of one tile block read its V in one L2
     const int L = xcd_remap((int)blockIdx.x, a.nwg);
-    const int kb32 = L % a.nkb;
+    const int kbl = L % a.nkb;
     const int bp0 = (L / a.nkb) * kGoT;
-    const int k0 = kb32 * kGoK;
+    const int k0 = kbl * G::kK;
     const int r16 = lane & 15, g = lane >> 4;
 
     const __amdgpu_buffer_rsrc_t urs = go_rsrc(a.U, a.u_bytes);
@@ -91,15 +106,15 @@ void gemm_out_kernel(GoArgs a) {
     // read zeros through out-of-range offsets)
     const int kt0 = k0 >> 4;
     const bool bok = bp0 + r16 < a.BP;
-    f4 acc[8][2];
+    f4 acc[8][KB];
 #pragma unroll
     for (int s = 0; s < 8; s++)
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) acc[s][kb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    // operands of one 32-channel step: 24 16-byte loads per lane, all issued
-    // before the step's MFMAs; two steps in flight (double buffer)
+        for (int kb = 0; kb < KB; kb++) acc[s][kb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    // operands of one 32-channel step: 8 * (KB + 1) 16-byte loads per lane,
+    // all issued before the step's MFMAs; two steps in flight (double buffer)
     struct Ops {
-        h8 u[8][2];
+        h8 u[8][KB];
         h8 v[8];
     };
     const int nsteps = (a.Cp + 31) / 32;
@@ -111,7 +126,7 @@ void gemm_out_kernel(GoArgs a) {
         for (int s = 0; s < 8; s++) {
             const int p = 8 * wave + s;
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+            for (int kb = 0; kb < KB; kb++)
                 o.u[s][kb] = __builtin_bit_cast(
                     h8, __builtin_amdgcn_raw_buffer_load_b128(
                             urs, kt0 + kb < a.nkt ? lo : kGoOob,
@@ -125,44 +140,53 @@ void gemm_out_kernel(GoArgs a) {
 #pragma unroll
         for (int s = 0; s < 8; s++)
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
+            for (int kb = 0; kb < KB; kb++)
                 acc[s][kb] =
                     __builtin_amdgcn_mfma_f32_16x16x32_f16(o.u[s][kb], o.v[s], acc[s][kb], 0, 0, 0);
     };
-    Ops o0, o1;
-    load(0, o0);
-    for (int j = 0; j < nsteps; j += 2) {
-        load(j + 1, o1);  // past the last step: zero loads (out-of-range offsets)
-        multiply(o0);
-        if (j + 1 >= nsteps) break;
-        load(j + 2, o0);
-        multiply(o1);
+    if constexpr (KB == 2) {
+        Ops o0, o1;
+        load(0, o0);
+        for (int j = 0; j < nsteps; j += 2) {
+            load(j + 1, o1);  // past the last step: zero loads (out-of-range offsets)
+            multiply(o0);
+            if (j + 1 >= nsteps) break;
+            load(j + 2, o0);
+            multiply(o1);
+        }
+    } else {
+        for (int j = 0; j < nsteps; j++) {
+            Ops o;
+            load(j, o);
+            multiply(o);
+        }
     }
 
     // ---- M (fp16) to LDS, one 16-byte write per (k, tile) row and lane ----
     // lane (g, r16) holds M[k = 16 kb + 4 g + i][tile r16] for its 8 positions
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
+    for (int kb = 0; kb < KB; kb++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int kk = 16 * kb + 4 * g + i;
             h8 v;
 #pragma unroll
             for (int s = 0; s < 8; s++) v[s] = to_f16(acc[s][kb][i]);
-            const int mo = kNhwc ? r16 * kGoTileP + kk * kGoPitch : (kk * kGoT + r16) * kGoPitch;
+            const int mo =
+                kNhwc ? r16 * G::kTileP + kk * kGoPitch : (kk * kGoT + r16) * kGoPitch;
             *reinterpret_cast<h8*>(ms + mo + 8 * wave) = v;
         }
     __syncthreads();
 
     // ---- output transform: one (k, tile) pair per thread ----
     // NCHW: lanes over tiles (adjacent tiles of a row write adjacent 12-byte
-    // row pieces); channels-last: lanes over channels (64 contiguous bytes
-    // per pixel)
-    const int kk = kNhwc ? (tid & (kGoK - 1)) : (tid >> 4);
-    const int t = kNhwc ? (tid >> 5) : (tid & (kGoT - 1));
+    // row pieces); channels-last: lanes over channels (32 or 64 contiguous
+    // bytes per pixel). With KB = 1 the 256 pairs take half the threads.
+    const int kk = kNhwc ? (tid & (G::kK - 1)) : (tid >> 4);
+    const int t = kNhwc ? (tid / G::kK) : (tid & (kGoT - 1));
     const int k = k0 + kk, bp = bp0 + t;
-    if (k >= a.K || bp >= a.BP) return;  // no barrier follows
-    const int mo = kNhwc ? t * kGoTileP + kk * kGoPitch : (kk * kGoT + t) * kGoPitch;
+    if (kk >= G::kK || t >= kGoT || k >= a.K || bp >= a.BP) return;  // no barrier follows
+    const int mo = kNhwc ? t * G::kTileP + kk * kGoPitch : (kk * kGoT + t) * kGoPitch;
     h8 mv[8];
 #pragma unroll
     for (int ii = 0; ii < 8; ii++) mv[ii] = *reinterpret_cast<const h8*>(ms + mo + 8 * ii);
@@ -232,9 +256,11 @@ void gemm_out_kernel(GoArgs a) {
 
 }  // namespace
 
-int64_t gemm_out_grid(int K, int BP) {
-    return (int64_t)((BP + kGoT - 1) / kGoT) * ((K + kGoK - 1) / kGoK);
+int64_t gemm_out_grid(int K, int BP, int kb) {
+    return (int64_t)((BP + kGoT - 1) / kGoT) * ((K + 16 * kb - 1) / (16 * kb));
 }
+
+int gemm_out_kb(int K, int BP, int cus) { return gemm_out_grid(K, BP, 1) <= cus ? 1 : 2; }
 
 int64_t gemm_out_v_elems(int Cp, int64_t BP) {
     return (int64_t)64 * ((BP + kGoT - 1) / kGoT) * ((Cp + 31) / 32) * 512;
@@ -242,12 +268,13 @@ int64_t gemm_out_v_elems(int Cp, int64_t BP) {
 
 hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, int B, int K,
                            int Cp, int nh, int nw, int Ho, int Wo, hipStream_t s, Epilogue ep,
-                           bool nhwc) {
+                           bool nhwc, int kb) {
+    if (kb != 1 && kb != 2) return hipErrorInvalidValue;
     const int64_t BP = (int64_t)B * nh * nw;
     const int64_t u_bytes = 2 * u_frag_elems(K, Cp);
     const int64_t v_bytes = 2 * gemm_out_v_elems(Cp, BP);
     const int64_t y_bytes = 2 * (int64_t)B * K * Ho * Wo;
-    const int64_t grid = gemm_out_grid(K, (int)BP);
+    const int64_t grid = gemm_out_grid(K, (int)BP, kb);
     if (Cp % 8 != 0 || u_bytes >= ((int64_t)1 << 31) || v_bytes >= ((int64_t)1 << 31) ||
         y_bytes >= ((int64_t)1 << 31) || grid >= ((int64_t)1 << 31))
         return hipErrorInvalidValue;
@@ -266,7 +293,7 @@ hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, i
     a.nw = nw;
     a.Ho = Ho;
     a.Wo = Wo;
-    a.nkb = (K + kGoK - 1) / kGoK;
+    a.nkb = (K + 16 * kb - 1) / (16 * kb);
     a.nkt = (K + 15) / 16;
     a.nbb = (int)((BP + kGoT - 1) / kGoT);
     a.y_pairs = (Wo % 2 == 0 &&
@@ -280,10 +307,17 @@ hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, i
     const dim3 g((unsigned)grid), blk(kGoThreads);
     a.nwg = (int)g.x;
     auto go = [&](auto kernel) { launch(kernel, g, blk, s, a); };
-    if (epilogue_needed(ep.bias, ep.relu, ep.residual))
-        nhwc ? go(gemm_out_kernel<true, true>) : go(gemm_out_kernel<false, true>);
+    auto pick = [&](auto kbc) {
+        constexpr int KB = decltype(kbc)::value;
+        if (epilogue_needed(ep.bias, ep.relu, ep.residual))
+            nhwc ? go(gemm_out_kernel<KB, true, true>) : go(gemm_out_kernel<KB, false, true>);
+        else
+            nhwc ? go(gemm_out_kernel<KB, true, false>) : go(gemm_out_kernel<KB, false, false>);
+    };
+    if (kb == 2)
+        pick(std::integral_constant<int, 2>());
     else
-        nhwc ? go(gemm_out_kernel<true, false>) : go(gemm_out_kernel<false, false>);
+        pick(std::integral_constant<int, 1>());
     return hipGetLastError();
 }
 

@@ -207,14 +207,17 @@ hipError_t launch_fused_small(const uint16_t* x, const uint16_t* U, uint16_t* y,
                               Epilogue ep = Epilogue(), bool nhwc = false);
 
 // Two-pass forward, second pass (path 6): the products and the output
-// transform of 16 tiles x 32 output channels per workgroup, U from the
+// transform of 16 tiles x 16 kb output channels per workgroup, U from the
 // launch_u_wfrag blocks and V in the two-pass layout (launch_input_transform
 // with vfrag = ceil(Cp / 32)); M stays in LDS.
-int64_t gemm_out_grid(int K, int BP);
+// kb: 16-row tiles of U per workgroup (2: 32 output channels, one workgroup
+// per CU; 1: 16 output channels, two per CU)
+int64_t gemm_out_grid(int K, int BP, int kb = 2);
+int gemm_out_kb(int K, int BP, int cus);  // the kb launch_gemm_out takes on a chip of cus CUs
 int64_t gemm_out_v_elems(int Cp, int64_t BP);  // V halves of the two-pass layout
 hipError_t launch_gemm_out(const uint16_t* Uw, const uint16_t* V, uint16_t* y, int B, int K,
                            int Cp, int nh, int nw, int Ho, int Wo, hipStream_t s, Epilogue ep,
-                           bool nhwc);
+                           bool nhwc, int kb = 2);
 
 // Input transform fused into the products (path 7), for GEMV-like shapes
 // (few tiles, many channels): workgroup = position row x group of nt <= 16

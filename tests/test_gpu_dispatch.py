@@ -56,7 +56,8 @@ def _forward(lib, path, x, w, pad):
 
 
 # (B, C, K, H, expected automatic path): the small-problem kernel (5) while
-# its grid is at most two workgroups per CU, else the library's cost model,
+# its grid is at most two workgroups per CU (four with two 32-channel chunks,
+# two and a half where the two-pass path can run), else the library's cost model,
 # fused ~(3 + 10 us per 32-channel chunk) per wave of workgroups against
 # three-pass ~10 us + its bytes at 5 TB/s
 AUTO_CASES = [
@@ -86,8 +87,9 @@ AUTO_CASES = [
     (1, 64, 64, 56, 5),    # B=1: the small-problem kernel (200 workgroups)
     (2, 64, 64, 56, 5),    # 400 workgroups
     (3, 64, 64, 56, 5),    # 600 workgroups, two 32-channel chunks: 12.3 vs 14.2 us
-    (4, 64, 64, 56, 5),    # 800 workgroups: 14.7 vs 15.2 us (two-pass)
-    (1, 64, 64, 112, 5),   # 724 workgroups: 13.3 vs 14.9 us
+    (4, 64, 64, 56, 6),    # 800 small-kernel workgroups (3.1 per CU): two-pass 12.8 vs 14.5 us
+    (1, 64, 64, 112, 6),   # 724 (2.8 per CU): two-pass 12.3 vs 13.4 us
+    (1, 48, 48, 112, 5),   # 543 (2.1 per CU): small kernel 12.1 vs two-pass 11.9 us, a near tie
     (2, 64, 64, 112, 6),   # 1448 workgroups: small kernel 21.4 vs two-pass 16.2 us
     (32, 48, 40, 13, 5),   # small images: 480 workgroups
     (1, 128, 128, 28, 7),  # conv3_x B=1: input transform in the products, 8.8 vs 9.3 us

@@ -1,8 +1,10 @@
 """Two-pass path (nova_set_path(h, 6)): the three-pass input transform, then
 the 64 Winograd-domain products and the output transform in one launch
-(gemm_out_kernel: 16 tiles x 32 output channels per workgroup, M kept in
-LDS; V written by the input transform in 1 KB operand blocks of 16 tiles x
-32 channels, U copied into the same block order). The products use the three-pass GEMM's lane layout
+(gemm_out_kernel: 16 tiles x 32 output channels per workgroup, or 16 output
+channels and two workgroups per CU where the grid has at most one such
+workgroup per CU; M kept in LDS; V written by the input transform in 1 KB
+operand blocks of 16 tiles x 32 channels, U copied into the same block
+order). The products use the three-pass GEMM's lane layout
 and channel order and the output transform its chains, so y must equal
 path 1 bit for bit -- for K and C off the 16/32 blocks, tile blocks that cross image
 boundaries, pads 0-2, channels-last, the bias/residual/ReLU epilogue and
@@ -61,8 +63,11 @@ CASES = [  # (B, C, K, H, W, pad)
     (4, 256, 40, 14, 14, 1),    # eight channel steps
     (7, 64, 100, 9, 11, 1),     # tiles of several images per block, K = 100
     (32, 128, 256, 14, 14, 1),  # K = 256 (automatic above 128 output channels)
-    (6, 64, 200, 28, 28, 1),    # K = 200: a partial last 32-channel output block
+    (6, 64, 200, 28, 28, 1),    # K = 200: a partial last 16-channel output block
+    (16, 64, 200, 28, 28, 1),   # 32 channels per workgroup, partial last 32-channel block
 ]
+# every case above but the first, the 128 -> 256 one and the last runs 16
+# output channels per workgroup on a 256-CU chip (grid at 16 channels <= CUs)
 
 
 @pytest.mark.parametrize("B,C,K,H,W,pad", CASES)
@@ -85,7 +90,8 @@ def test_two_pass_equals_three_pass(oracle, B, C, K, H, W, pad):
     assert oracle.max_abs(yg, yo) <= 0.25
 
 
-@pytest.mark.parametrize("B,C,K,H,pad", [(4, 128, 128, 28, 1), (3, 64, 40, 13, 0)])
+@pytest.mark.parametrize("B,C,K,H,pad", [(4, 128, 128, 28, 1), (3, 64, 40, 13, 0),
+                                         (32, 128, 128, 28, 1)])
 def test_two_pass_channels_last_and_epilogue(B, C, K, H, pad):
     print(f"[two-pass nhwc] B={B} C={C} K={K} H={H} pad={pad}", flush=True)
     torch.manual_seed(43)
