@@ -256,7 +256,7 @@ __device__ __forceinline__ void v_row_phase(const InGemmArgs& a, const TileOrigi
 
 // KR: 16-row output-channel tiles per workgroup; NSM: the most 32-channel
 // steps this instantiation holds (nsteps <= NSM).
-template <int KR, int NSM, bool kNhwc>
+template <int KR, int NSM, bool kNhwc, int kPol>
 __global__ __launch_bounds__(kIT, 1) void in_gemm_kernel(InGemmArgs a) {
     __shared__ __align__(16) _Float16 vs[8 * kMaxTiles * (NSM * 32 + 8)];
     __shared__ TileOrigin to[kMaxTiles];
@@ -358,13 +358,13 @@ __global__ __launch_bounds__(kIT, 1) void in_gemm_kernel(InGemmArgs a) {
         if (vec_store) {
             h4 v = {(_Float16)acc[kt][0], (_Float16)acc[kt][1], (_Float16)acc[kt][2],
                     (_Float16)acc[kt][3]};
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), mrs, off, mu, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), mrs, off, mu, kPol);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++)
                 __builtin_amdgcn_raw_buffer_store_b16(
                     __builtin_bit_cast(uint16_t, (_Float16)acc[kt][i]), mrs,
-                    (sok && k + i < a.K) ? 2 * (bp * a.K + k + i) : kIOob, mu, 0);
+                    (sok && k + i < a.K) ? 2 * (bp * a.K + k + i) : kIOob, mu, kPol);
         }
     }
 }
@@ -474,22 +474,32 @@ hipError_t launch_in_gemm(const uint16_t* x, const uint16_t* Uw, uint16_t* M, in
     const dim3 grid((unsigned)p.grid), block(kIT);
     a.nwg = (int)grid.x;
     auto go = [&](auto kernel) { launch(kernel, grid, block, s, a); };
-    auto pick = [&](auto nh_) {
+    // M (8-byte pieces of lines) written through the L2 while it is small
+    // (kWTSmallBytes; conv3_x batch 1 8.81 -> 8.66 us in a graph)
+    const bool wt = m_bytes <= kWTSmallBytes;
+    auto pick = [&](auto nh_, auto pol_) {
         constexpr bool kN = decltype(nh_)::value;
+        constexpr int P = decltype(pol_)::value;
         if (p.kr == 1) {
-            if (p.nsm == 4) go(in_gemm_kernel<1, 4, kN>);
-            else if (p.nsm == 8) go(in_gemm_kernel<1, 8, kN>);
-            else go(in_gemm_kernel<1, 16, kN>);
+            if (p.nsm == 4) go(in_gemm_kernel<1, 4, kN, P>);
+            else if (p.nsm == 8) go(in_gemm_kernel<1, 8, kN, P>);
+            else go(in_gemm_kernel<1, 16, kN, P>);
         } else {
-            if (p.nsm == 4) go(in_gemm_kernel<2, 4, kN>);
-            else if (p.nsm == 8) go(in_gemm_kernel<2, 8, kN>);
-            else go(in_gemm_kernel<2, 16, kN>);
+            if (p.nsm == 4) go(in_gemm_kernel<2, 4, kN, P>);
+            else if (p.nsm == 8) go(in_gemm_kernel<2, 8, kN, P>);
+            else go(in_gemm_kernel<2, 16, kN, P>);
         }
     };
+    auto by_policy = [&](auto nh_) {
+        if (wt)
+            pick(nh_, std::integral_constant<int, kWT>());
+        else
+            pick(nh_, std::integral_constant<int, 0>());
+    };
     if (nhwc)
-        pick(std::true_type());
+        by_policy(std::true_type());
     else
-        pick(std::false_type());
+        by_policy(std::false_type());
     return hipGetLastError();
 }
 

@@ -107,11 +107,35 @@ hipError_t launch_u_frag(const uint16_t* U, uint16_t* Uf, int K, int Cp, hipStre
 // same size as the fused kernels' copy).
 hipError_t launch_u_wfrag(const uint16_t* U, uint16_t* Uw, int K, int Cp, hipStream_t s);
 
+// Cache-policy operands of buffer stores. kNt (non-temporal) marks the lines
+// for early eviction, but they still reach the L2 dirty. kWT (sc1, device
+// scope) writes through the L2 to the memory side: the kernel's end then has
+// no dirty lines to write back before the next launch may start. Measured on
+// MI355X (a kernel that only stores, then an empty kernel; us, the stores'
+// span + the gap to the next kernel's first wave): 16.8 MB write-back 1.92 +
+// 2.39, nt 1.92 + 2.40, write-through 2.92 + 1.01; 50 MB 5.72 + 3.36 against
+// 7.45 + 1.00; with nothing written the gap is 1.0-1.1. It pays where every
+// store instruction of a wave writes whole 128-byte lines and the stores
+// overlap the kernel's arithmetic: the V of the tile-block transforms in the
+// product layout and of the run form, and the staged M tiles of the GEMM.
+// Partial lines written through reach memory piece by piece (the
+// lane-parallel and two-pass-layout tile-block V: 64@56^2 batch 8 two-pass
+// 13.8 -> 16.3 us in a graph, SD-1.5 640@32^2 batch 2 (5.9 MB of V) 27.9 ->
+// 29.8; the fused kernels' y rows: conv2_x batch 32 21.5 -> 26.6), except
+// when they are few: partial-line V and M of at most kWTSmallBytes (batch-1
+// layers) are written through too.
+constexpr int kNt = 2;
+constexpr int kWT = 16;
+constexpr int64_t kWTSmallBytes = (int64_t)2 << 20;
+
 // ---- input transform -----------------------------------------------------
 // V[p*pstride + bp*ldv + c], bp = (b*nh + th)*nw + tw, for th < nh, tw < nw.
 // Channels c in [C, ldv) are written as zero. x is NCHW, or NHWC if nhwc.
-// stream_v: the tile-block forms store V with the non-temporal (nt) cache
-// policy (results unchanged; see wgemm_v_reads for when it pays).
+// V store cache policy (results unchanged): the forms whose wave stores are
+// whole 128-byte lines (the tile-block forms in the product layout with at
+// least 64 channels per workgroup and ldv % 64 == 0, and the run form) write
+// through the L2; otherwise stream_v asks for the non-temporal (nt) policy
+// (see wgemm_v_reads for when it pays).
 // vfrag: 0 = V in the product layout V[p][bp][ldv]; otherwise the number of
 // 32-channel chunks of the two-pass layout (1 KB MFMA B-operand blocks of 16
 // tiles x 32 channels; pstride = ceil(BP / 16) * vfrag * 512 halves).

@@ -12,6 +12,7 @@
 //   input   /root/reference/csrc/nova_winograd.hip:336-392 (fused zero padding :368-370)
 //   output  /root/reference/csrc/nova_winograd.hip:398-450 (masking of h>=Ho, w>=Wo)
 #include <algorithm>
+#include <type_traits>
 
 #include "nova_internal.h"
 #include "nova_tables.h"
@@ -156,11 +157,6 @@ hipError_t launch_u_wfrag(const uint16_t* U, uint16_t* Uw, int K, int Cp, hipStr
 // per-access vector address arithmetic).
 // ---------------------------------------------------------------------------
 constexpr int kOob = (int)0x80000000;  // byte offset beyond any buffer used here
-// Cache-policy operand of a buffer store that streams past the L2 (nt). The
-// tile-block input transforms write V in whole 128-byte lines (64 lanes x 2
-// bytes); streamed, V goes to the memory-side cache without filling the L2
-// with dirty lines that the kernel's end would have to write back.
-constexpr int kNt = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
@@ -261,7 +257,7 @@ __device__ __forceinline__ void input_stage(unsigned char* sx, __amdgpu_buffer_r
         }
 }
 
-template <int TW, bool kStream>
+template <int TW, int kPol>
 __global__ __launch_bounds__(256) void input_transform_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int xd,
@@ -345,7 +341,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
         [&](int r, int s, float v) {
             const int p = r * 8 + s;
             __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, to_f16(v)), vrs,
-                                                  voff, (int)(2 * p * pstride), kStream ? kNt : 0);
+                                                  voff, (int)(2 * p * pstride), kPol);
         });
 }
 
@@ -361,7 +357,7 @@ __global__ __launch_bounds__(256) void input_transform_kernel(
 // kernel. Zero padding is already in LDS, so no masks. Needs C % 8 == 0 and a
 // 16-byte aligned x (the launcher checks; otherwise the lane-parallel form).
 // ---------------------------------------------------------------------------
-template <int TW, bool kStream>
+template <int TW, int kPol>
 __global__ __launch_bounds__(256) void input_nhwc_kernel(
     const _Float16* __restrict__ x, _Float16* __restrict__ V, int C, int H, int W, int pad,
     int nh, int nw, int ldv, int64_t pstride, int cblocks, int x_bytes, int64_t v_bytes,
@@ -415,7 +411,7 @@ __global__ __launch_bounds__(256) void input_nhwc_kernel(
                         const int p = r * 8 + s2;
                         __builtin_amdgcn_raw_buffer_store_b16(
                             __builtin_bit_cast(uint16_t, to_f16(v)), vrs, voff,
-                            (int)(2 * p * pstride), kStream ? kNt : 0);
+                            (int)(2 * p * pstride), kPol);
                     });
 }
 
@@ -436,7 +432,7 @@ __global__ __launch_bounds__(256) void input_nhwc_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kLpPitch = 72;  // floats per channel in the transpose buffer
 
-template <bool kNhwc>
+template <bool kNhwc, int kPol>
 __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restrict__ x,
                                                        _Float16* __restrict__ V, int C, int H,
                                                        int W, int pad, int nh, int nw, int ldv,
@@ -491,7 +487,7 @@ __global__ __launch_bounds__(256) void input_lp_kernel(const _Float16* __restric
         for (int q = 0; q < 8; q++)
             if (kBh[q][s] != 0.0f) acc = __builtin_fmaf(t[q], kBh[q][s], acc);
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, to_f16(acc)), vrs,
-                                              voff, (int)(2 * s * pstride), 0);
+                                              voff, (int)(2 * s * pstride), kPol);
     }
 }
 
@@ -503,14 +499,20 @@ static hipError_t launch_input_lp(const uint16_t* x, uint16_t* V, int B, int C, 
     if (items >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
     const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
+    // a wave's stores are 16-byte pieces of 8 lines: written through the L2
+    // only while V is small (whole forwards in a graph, us: conv4_x batch 1
+    // 9.22 -> 9.00, conv5_x 11.71 -> 11.46, SD-1.5 1280@8^2 batch 2 (1.3 MB)
+    // 38.7 -> 38.4; at 2.5-5.9 MB it lost 0.5-2 us)
+    const bool wt = 2 * 64 * pstride <= kWTSmallBytes;
+    auto go = [&](auto kernel) {
+        launch_n(kernel, dim3((unsigned)items), dim3(256), s,
+                 reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W,
+                 pad, nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
+    };
     if (nhwc)
-        launch_n(input_lp_kernel<true>, dim3((unsigned)items), dim3(256), s,
-            reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
-            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
+        wt ? go(input_lp_kernel<true, kWT>) : go(input_lp_kernel<true, 0>);
     else
-        launch_n(input_lp_kernel<false>, dim3((unsigned)items), dim3(256), s,
-            reinterpret_cast<const _Float16*>(x), reinterpret_cast<_Float16*>(V), C, H, W, pad,
-            nh, nw, ldv, pstride, ncg, (int)x_bytes, 2 * 64 * pstride, vfrag);
+        wt ? go(input_lp_kernel<false, kWT>) : go(input_lp_kernel<false, 0>);
     return hipGetLastError();
 }
 
@@ -546,8 +548,8 @@ static int pick_tw(int64_t rows, int n, int ch) {
 // workgroup takes 16 consecutive tiles (bp, across tile rows and images:
 // one block column) x 16 channels; wave w holds tiles 8*(w & 1) .. +7 x
 // channels 8*(w >> 1) .. +7 of them, lane = (tile % 8, channel % 8), so each
-// store instruction writes one whole line of a position's block (streamed
-// past the L2 when kStream). Each thread loads its patch's 8 rows straight
+// store instruction writes one whole line of a position's block (written
+// through the L2, kWT). Each thread loads its patch's 8 rows straight
 // from global memory (a 16-byte and a 4-byte load from the dword at or below
 // the row start, shifted by 0 or 2 bytes; rows outside the image and
 // channels past C read zero; a row starting before x_al, only the tensor's
@@ -555,7 +557,7 @@ static int pick_tw(int64_t rows, int n, int ch) {
 // masks the columns outside the image and runs the shared chains: V is the
 // tile-block kernel's, bit for bit. NCHW only.
 // ---------------------------------------------------------------------------
-template <bool kStream>
+template <int kPol>
 __global__ __launch_bounds__(256) void input_run_kernel(
     const void* __restrict__ x_al, _Float16* __restrict__ V, int C, int Cp, int H, int W,
     int pad, int nw, int P, int BP, int ncg, int vfrag, int64_t pstride, int x_bytes, int xd,
@@ -643,13 +645,13 @@ __global__ __launch_bounds__(256) void input_run_kernel(
         [&](int r, int s2, float v) {
             const int p = r * 8 + s2;
             __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, to_f16(v)), vrs,
-                                                  voff, (int)(2 * p * pstride), kStream ? kNt : 0);
+                                                  voff, (int)(2 * p * pstride), kPol);
         });
 }
 
 static hipError_t launch_input_run(const uint16_t* x, uint16_t* V, int B, int C, int H, int W,
                                    int pad, int nh, int nw, int ldv, int64_t pstride,
-                                   hipStream_t s, bool stream_v, int vfrag) {
+                                   hipStream_t s, int vfrag) {
     const int P = nh * nw;
     const int64_t BP = (int64_t)B * P;
     const int ncg = (ldv + 15) / 16;
@@ -666,10 +668,7 @@ static hipError_t launch_input_run(const uint16_t* x, uint16_t* V, int B, int C,
                C, ldv, H, W, pad, nw, P, (int)BP, ncg, vfrag, pstride, (int)x_bytes, xd,
                2 * 64 * pstride);
     };
-    if (stream_v)
-        go(input_run_kernel<true>);
-    else
-        go(input_run_kernel<false>);
+    go(input_run_kernel<kWT>);
     return hipGetLastError();
 }
 
@@ -697,13 +696,13 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     // batch 32 24.25 vs 23.41 (input transform 8.78 vs 7.77), batch 24 22.75
     // vs 21.94; 96@28^2 batch 32 19.91 vs 18.85; 48->40@13^2 batch 128 17.09
     // vs 15.92; 128->256@14^2 batch 32 (144 workgroups) 21.18 vs 21.03; with
-    // few workgroups it loses: 128@28^2 batch 3 (40) 17.49 vs 18.44). Its V
-    // stays in the L2 for the products kernel (the workgroups of a tile
-    // block sit on the same XCD in both grids): streamed past it, the input
-    // transform ran 1 us faster but the products 1.4 us slower.
+    // few workgroups it loses: 128@28^2 batch 3 (40) 17.49 vs 18.44). Its
+    // whole-line V stores write through the L2 (kWT): conv3_x batch 32 23.69
+    // -> 22.39 us in a graph (streamed with nt instead, the input transform
+    // ran 1 us faster but the products 1.4 us slower).
     if (!nhwc && vfrag > 0 && pad <= 4 &&
         ((int64_t)B * nh * nw + 15) / 16 * ((ldv + 15) / 16) >= 256)
-        return launch_input_run(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, false, vfrag);
+        return launch_input_run(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, vfrag);
     if (latency_bound((int64_t)B * nh, nw, ldv) ||
         (nhwc && (C % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0)))
         return launch_input_lp(x, V, B, C, H, W, pad, nh, nw, ldv, pstride, s, nhwc, vfrag);
@@ -714,20 +713,42 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     if (nblocks >= ((int64_t)1 << 31)) return hipErrorInvalidConfiguration;
     const dim3 grid((unsigned)nblocks), block(256);
     _Float16* Vh = reinterpret_cast<_Float16*>(V);
+    // V stores: a wave writes 64 consecutive channels of one (tile,
+    // position) -- whole 128-byte lines in the product layout when the
+    // workgroup holds at least 64 channels and rows are whole lines -- written
+    // through the L2 (kWT); otherwise nt when the GEMM reads V few times
+    // (stream_v), else write-back. Whole forwards in a graph, us, before ->
+    // after: ResNet-50 batch 32 256@14^2 25.75 -> 24.49, 512@7^2 25.42 ->
+    // 23.24; batch 128 256@14^2 49.4 -> 45.8; SD-1.5 320@64^2 batch 2 28.3 ->
+    // 25.7, 640->320@64^2 34.2 -> 31.7; SDXL 320@128^2 38.0 -> 35.3.
+    const bool whole_lines = vfrag == 0 && tw <= 4 && ldv % 64 == 0;
+    const int pol = whole_lines ? kWT : stream_v ? kNt : 0;
+    auto by_policy = [&](auto tw_c, auto go) {
+        constexpr int T = decltype(tw_c)::value;
+        if (pol == kWT)
+            go(std::integral_constant<int, T>(), std::integral_constant<int, kWT>());
+        else if (pol == kNt)
+            go(std::integral_constant<int, T>(), std::integral_constant<int, kNt>());
+        else
+            go(std::integral_constant<int, T>(), std::integral_constant<int, 0>());
+    };
+    auto by_tw = [&](auto go) {
+        if (tw == 2)
+            by_policy(std::integral_constant<int, 2>(), go);
+        else if (tw == 4)
+            by_policy(std::integral_constant<int, 4>(), go);
+        else
+            by_policy(std::integral_constant<int, 8>(), go);
+    };
     if (nhwc) {
         const int64_t x_bytes = 2 * (int64_t)B * C * H * W;
         if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
         const _Float16* xh = reinterpret_cast<const _Float16*>(x);
-        auto go = [&](auto kernel) {
-            launch_n(kernel, grid, block, s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
-                   (int)x_bytes, 2 * 64 * pstride, vfrag);
-        };
-        if (tw == 2)
-            stream_v ? go(input_nhwc_kernel<2, true>) : go(input_nhwc_kernel<2, false>);
-        else if (tw == 4)
-            stream_v ? go(input_nhwc_kernel<4, true>) : go(input_nhwc_kernel<4, false>);
-        else
-            stream_v ? go(input_nhwc_kernel<8, true>) : go(input_nhwc_kernel<8, false>);
+        by_tw([&](auto tw_c, auto pol_c) {
+            launch_n(input_nhwc_kernel<decltype(tw_c)::value, decltype(pol_c)::value>, grid, block,
+                     s, xh, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks, (int)x_bytes,
+                     2 * 64 * pstride, vfrag);
+        });
         return hipGetLastError();
     }
     // x is addressed from the 16-byte boundary at or below it (same granule,
@@ -737,16 +758,11 @@ hipError_t launch_input_transform(const uint16_t* x, uint16_t* V, int B, int C, 
     const int64_t x_bytes = dword_ceil(2 * (int64_t)B * C * H * W + xd);
     if (x_bytes >= ((int64_t)1 << 31) - 64) return hipErrorInvalidValue;
     const void* xa = reinterpret_cast<const void*>(xp - (uintptr_t)xd);
-    auto go = [&](auto kernel) {
-        launch_n(kernel, grid, block, s, xa, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks,
-               (int)x_bytes, xd, 2 * 64 * pstride, vfrag);
-    };
-    if (tw == 2)
-        stream_v ? go(input_transform_kernel<2, true>) : go(input_transform_kernel<2, false>);
-    else if (tw == 4)
-        stream_v ? go(input_transform_kernel<4, true>) : go(input_transform_kernel<4, false>);
-    else
-        stream_v ? go(input_transform_kernel<8, true>) : go(input_transform_kernel<8, false>);
+    by_tw([&](auto tw_c, auto pol_c) {
+        launch_n(input_transform_kernel<decltype(tw_c)::value, decltype(pol_c)::value>, grid,
+                 block, s, xa, Vh, C, H, W, pad, nh, nw, ldv, pstride, cblocks, (int)x_bytes, xd,
+                 2 * 64 * pstride, vfrag);
+    });
     return hipGetLastError();
 }
 

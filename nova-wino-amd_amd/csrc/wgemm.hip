@@ -14,6 +14,8 @@
 // multiple of 8 and zero padded, so partial 32-channel steps only mask whole
 // 8-channel groups. No atomics, no split-K: results are deterministic.
 // Byte offsets are 32-bit: U, V and M must each stay below 2 GB.
+#include <type_traits>
+
 #include "nova_internal.h"
 #include "nova_tile_math.h"
 
@@ -290,8 +292,8 @@ __global__ __launch_bounds__(64 * WK * WB) void wgemm_lds_kernel(const _Float16*
     const int mu = 2 * p * BP * K;
     if constexpr (SM != 0) {
         // SM 1/2: the M tile goes through LDS as [bp][k] rows and leaves as
-        // whole rows, 16 bytes per lane (SM 2: with the nt cache policy); the
-        // L2 then holds whole dirty lines instead of 32-byte pieces of 16.
+        // whole rows, 16 bytes per lane (SM 2: written through the L2, sc1);
+        // the L2 then holds whole lines instead of 32-byte pieces of 16.
         if ((K & 7) == 0) {
             constexpr int kMP = TK + 8;  // halves per staged row
             static_assert(TB * kMP <= 2 * (TK + TB) * kStageC, "M tile fits in the stages");
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(64 * WK * WB) void wgemm_lds_kernel(const _Float16*
                 const int bp = n0 + row, k = k0 + 8 * ch;
                 const u4 v = *reinterpret_cast<const u4*>(sm + row * kMP + 8 * ch);
                 __builtin_amdgcn_raw_buffer_store_b128(
-                    v, mrs, (bp < BP && k < K) ? 2 * (bp * K + k) : kOob, mu, SM == 2 ? 2 : 0);
+                    v, mrs, (bp < BP && k < K) ? 2 * (bp * K + k) : kOob, mu, SM == 2 ? kWT : 0);
             }
             return;
         }
@@ -344,16 +346,21 @@ __global__ __launch_bounds__(64 * WK * WB) void wgemm_lds_kernel(const _Float16*
 }
 
 // M epilogue of the LDS kernels (SM of wgemm_lds_kernel): always staged
-// through LDS as whole rows (K % 8 == 0); stored with the nt cache policy
-// when M holds 4-16 MB. Measured on MI355X, whole forwards, us (direct b64
-// stores -> staged -> staged + nt): ResNet-50 batch 32 128@28^2 28.9 -> 28.0
-// -> 27.4, 256@14^2 30.2 -> 29.6 -> 28.4, 512@7^2 28.6 -> 27.1 -> 26.7,
-// conv2_x three-pass 40.8 -> 36.4 -> 37.0; batch 128 128@28^2 70.3 -> 64.1
-// -> 68.4; batch 1 64@56^2 10.9 -> 10.4 -> 10.7. Outside 4-16 MB the nt
-// stores were as often slower as faster.
+// through LDS as whole rows (K % 8 == 0); written through the L2 (sc1, so the
+// launch boundary has no dirty M to write back before the output transform
+// starts) when M holds at most 32 MB. Measured on MI355X, whole forwards, us
+// (direct b64 stores -> staged): ResNet-50 batch 32 128@28^2 28.9 -> 28.0,
+// 256@14^2 30.2 -> 29.6, 512@7^2 28.6 -> 27.1, conv2_x three-pass 40.8 ->
+// 36.4; batch 128 128@28^2 70.3 -> 64.1; batch 1 64@56^2 10.9 -> 10.4.
+// Staged, write-back -> written through (with the V of the input transform
+// written through as well; GEMM + output transform launches, event-timed):
+// batch 16 256@14^2 7.22 + 6.75 -> 6.42 + 5.95; batch 64 128@28^2 11.69 +
+// 11.69 -> 10.54 + 11.56; SDXL 320@128^2 (20 MB) 13.86 + 11.36 -> 12.81 +
+// 11.52; above 32 MB it loses (batch 128 512@7^2, 34 MB: 26.59 + 12.77 ->
+// 28.06 + 15.25). Streaming M with nt instead (4-16 MB) gained 0.4-1.2 us.
 static int m_epilogue(int K, int BP) {
     const int64_t m_bytes = 2 * (int64_t)64 * BP * K;
-    return (m_bytes >= (4 << 20) && m_bytes <= (16 << 20)) ? 2 : 1;
+    return m_bytes <= ((int64_t)32 << 20) ? 2 : 1;
 }
 
 template <int TK, int TB, int WK, int WB, int PF>
@@ -393,7 +400,7 @@ static hipError_t launch_lds(const uint16_t* U, const uint16_t* V, uint16_t* M, 
 // graph, us: 1280@32^2 batch 1 51.0 -> 49.0, 1280@36^2 51.7 -> 49.8; 1024@32^2
 // batch 1 36.3 -> 36.5).
 // ---------------------------------------------------------------------------
-template <int MT, int NT, int PD, int WPB>
+template <int MT, int NT, int PD, int WPB, int kPol>
 __global__ __launch_bounds__(64 * WPB) void wgemm_block_kernel(
     const _Float16* __restrict__ Uw, const _Float16* __restrict__ Vb, _Float16* __restrict__ M,
     int K, int Cp, int BP, int u_bytes, int v_bytes, int m_bytes, int nwg) {
@@ -467,13 +474,13 @@ __global__ __launch_bounds__(64 * WPB) void wgemm_block_kernel(
                 h4 v = {(_Float16)acc[i][n][0], (_Float16)acc[i][n][1], (_Float16)acc[i][n][2],
                         (_Float16)acc[i][n][3]};
                 __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, v), mrs,
-                                                      k < K ? off : kOob, mu, 0);
+                                                      k < K ? off : kOob, mu, kPol);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     __builtin_amdgcn_raw_buffer_store_b16(
                         __builtin_bit_cast(uint16_t, (_Float16)acc[i][n][e]), mrs,
-                        k + e < K ? off + 2 * e : kOob, mu, 0);
+                        k + e < K ? off + 2 * e : kOob, mu, kPol);
             }
         }
 }
@@ -496,12 +503,22 @@ hipError_t launch_wgemm_blocks(const uint16_t* Uw, const uint16_t* Vb, uint16_t*
                (int)(2 * u_frag_elems(K, Cp)), (int)(2 * gemm_out_v_elems(Cp, BP)),
                (int)(2 * (int64_t)64 * BP * K));
     };
-    if (BP <= 16)
-        go(wgemm_block_kernel<kMT, 1, kPD, kWPB>);
-    else if (BP <= 32)
-        go(wgemm_block_kernel<kMT, 2, kPD, kWPB>);
+    // M (32-byte pieces of lines) written through the L2 while it is small
+    // (batch-1 layers, kWTSmallBytes)
+    const bool wt = 2 * (int64_t)64 * BP * K <= kWTSmallBytes;
+    auto by_tiles = [&](auto pol) {
+        constexpr int P = decltype(pol)::value;
+        if (BP <= 16)
+            go(wgemm_block_kernel<kMT, 1, kPD, kWPB, P>);
+        else if (BP <= 32)
+            go(wgemm_block_kernel<kMT, 2, kPD, kWPB, P>);
+        else
+            go(wgemm_block_kernel<kMT, 3, kPD, kWPB, P>);
+    };
+    if (wt)
+        by_tiles(std::integral_constant<int, kWT>());
     else
-        go(wgemm_block_kernel<kMT, 3, kPD, kWPB>);
+        by_tiles(std::integral_constant<int, 0>());
     return hipGetLastError();
 }
 
