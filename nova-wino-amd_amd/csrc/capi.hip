@@ -395,18 +395,24 @@ bool two_pass_possible(int C, int K) { return C <= 128 && K <= 256 && 2 * K >= C
 // 16.8, B=20 28.2 vs 18.2; 128->192@14^2 B=48 26.1 vs 21.5): each two-pass
 // workgroup reads all Cp channels of its operands, so its time follows Cp,
 // not K. Grids of at most one 16-channel workgroup per CU run 16 output
-// channels per workgroup, two per CU (gemm_out_kb); at most 128 output
-// channels that admits grids of 64 such workgroups (us, three-pass vs
-// two-pass: 96@28^2 B=8, 78 workgroups, 14.10 vs 13.76; 128@28^2 B=8, 104:
-// 16.33 vs 15.95; 128@28^2 B=4, 56: 11.69 vs 14.74 stays three-pass).
+// channels per workgroup, two per CU (gemm_out_kb); at most 64 input
+// channels that admits grids of 64 such workgroups (64@56^2 B=4, 100
+// workgroups: small-problem kernel 14.5 vs 12.8 us; B=8, 200: three-pass 18.5
+// vs 13.8). With V and M written through the L2 (the three-pass path's two
+// launch boundaries got cheaper) the three-pass path moved ahead at 128
+// input channels below 128 such workgroups (128@28^2 B=8, 104: 15.49 vs
+// 15.91) and above 128 output channels below three quarters of the CUs
+// (128->256@14^2 B=32, 144: 20.49 vs 21.35; B=48, 216: 26.21 vs 24.14;
+// 128->256@28^2 B=16, 200: 24.62 vs 23.43).
 bool two_pass_wins(const Handle* Hd, const Shape& s) {
     if (!two_pass_possible(Hd->C, Hd->K)) return false;
     const int bp = (int)std::min<int64_t>(s.BP, INT32_MAX);
     const int64_t grid = gemm_out_grid(Hd->K, bp);
     const int64_t v_bytes = 2 * gemm_out_v_elems(Hd->Cp, s.BP);
     if (grid > Hd->cus || v_bytes > (int64_t)20 << 20) return false;
-    if (Hd->K > 128) return grid >= 128;
-    return gemm_out_grid(Hd->K, bp, gemm_out_kb(Hd->K, bp, Hd->cus)) >= 64;
+    if (Hd->K > 128) return 4 * grid >= 3 * (int64_t)Hd->cus;
+    const int64_t min_grid = Hd->Cp > 64 ? 128 : 64;
+    return gemm_out_grid(Hd->K, bp, gemm_out_kb(Hd->K, bp, Hd->cus)) >= min_grid;
 }
 
 bool in_gemm_plan_for(const Handle* Hd, const Shape& s, InGemmPlan* p) {

@@ -81,7 +81,9 @@ AUTO_CASES = [
     (64, 128, 128, 28, 1),  # 400 workgroups (a second round): three-pass 36.7 vs 41.5 us
     (32, 128, 64, 28, 6),   # K = C / 2: two-pass 22.6 vs 24.1 us
     (32, 128, 32, 28, 1),   # K < C / 2: three-pass
-    (32, 128, 256, 14, 6),  # 144 workgroups: two-pass 21.0 vs three-pass 23.7 us
+    (32, 128, 256, 14, 1),  # 144 workgroups (under 3/4 of the CUs): three-pass 20.5 vs two-pass 21.4 us
+    (48, 128, 256, 14, 6),  # 216 workgroups: two-pass 24.1 vs three-pass 26.2 us
+    (8, 128, 128, 28, 1),   # 104 16-channel workgroups at 128 input channels: 15.5 vs 15.9 us
     (16, 128, 256, 14, 1),  # 72 workgroups above 128 output channels: 18.2 vs 20.0 us
     (32, 128, 512, 7, 1),   # more than 256 output channels: three-pass
     (1, 64, 64, 56, 5),    # B=1: the small-problem kernel (200 workgroups)

@@ -62,7 +62,7 @@ CASES = [  # (B, C, K, H, W, pad)
     (1, 3, 48, 30, 30, 1),      # C = 3 (one 8-channel group)
     (4, 256, 40, 14, 14, 1),    # eight channel steps
     (7, 64, 100, 9, 11, 1),     # tiles of several images per block, K = 100
-    (32, 128, 256, 14, 14, 1),  # K = 256 (automatic above 128 output channels)
+    (32, 128, 256, 14, 14, 1),  # K = 256 (automatic above 128 output channels from 192 workgroups)
     (6, 64, 200, 28, 28, 1),    # K = 200: a partial last 16-channel output block
     (16, 64, 200, 28, 28, 1),   # 32 channels per workgroup, partial last 32-channel block
 ]

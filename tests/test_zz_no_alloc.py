@@ -60,7 +60,8 @@ def _pair(lib, h, x, K, pad=1, nhwc=False):
 # nova_forward_noalloc) pair where the allocation-free form runs three-pass
 # in place of the two-pass path (bit-identical to it)
 CASES = [
-    (128, 128, 28, 1, 8, 3, ((6, 1), 1)),  # conv3_x: two-pass / three-pass, then three-pass
+    (128, 128, 28, 1, 8, 3, 1),     # three-pass, conv3_x
+    (64, 64, 56, 1, 4, 2, ((6, 1), 5)),  # two-pass / three-pass, then the small-problem kernel
     (64, 64, 56, 1, 32, 24, 3),     # fused tile-block, conv2_x (no workspace)
     (512, 512, 7, 1, 32, 1, 1),     # three-pass, conv5_x, then batch 1
     (100, 24, 17, 0, 6, 2, (1, 7)),  # C % 8 != 0 (padded channel pitch), pad 0; batch 2
