@@ -21,18 +21,25 @@ struct KernelEvents {
 };
 KernelEvents& kernel_events();
 
+// lds: bytes of dynamic LDS (extern __shared__) per workgroup.
 template <typename... KArgs, typename... Args>
-inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
-                   Args... args) {
+inline void launch_lds(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds,
+                       hipStream_t s, Args... args) {
     static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
     KernelEvents& ev = kernel_events();
     if (ev.start != nullptr || ev.stop != nullptr) {
-        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev.start, ev.stop, 0,
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, s, ev.start, ev.stop, 0,
                               static_cast<KArgs>(args)...);
         ev = KernelEvents{};
     } else {
-        kernel<<<grid, block, 0, s>>>(static_cast<KArgs>(args)...);
+        kernel<<<grid, block, lds, s>>>(static_cast<KArgs>(args)...);
     }
+}
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+                   Args... args) {
+    launch_lds(kernel, grid, block, 0, s, args...);
 }
 
 // launch() for a kernel with a one-dimensional grid whose last parameter is
@@ -45,6 +52,13 @@ template <typename... KArgs, typename... Args>
 inline void launch_n(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
                      Args... args) {
     launch(kernel, grid, block, s, args..., (int)grid.x);
+}
+// launch_n() with dynamic LDS and the workgroup's thread count (block.x)
+// appended before the workgroup count.
+template <typename... KArgs, typename... Args>
+inline void launch_n_lds(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds,
+                         hipStream_t s, Args... args) {
+    launch_lds(kernel, grid, block, lds, s, args..., (int)block.x, (int)grid.x);
 }
 
 // Error codes returned by nova_get_last_error().

@@ -107,9 +107,14 @@ def test_input_transform_bitexact(oracle, B, C, H, W, pad):
 # Output: the lane-parallel kernel below 256 tile-block workgroups, and for
 # an odd row pitch on images at most two tiles wide below 640 ((16, 512, 7,
 # 7)); the tile-block kernel for (8, 64, 56, 56) and, odd rows, (12, 130, 27,
-# 29) and (32, 130, 27, 29).
+# 29) and (32, 130, 27, 29); the image-block kernel (whole images per
+# workgroup, 16-byte span stores) for (32, 256, 14, 14) (32 channels per
+# workgroup, 16 reference tiles per image, dead ones included), (32, 512, 7,
+# 7) (64, odd rows) and (32, 200, 14, 14) (16 channels, a partial last
+# channel block).
 OUTPUT_CASES = [(1, 64, 56, 56), (2, 48, 14, 14), (1, 130, 7, 9), (3, 8, 13, 11), (1, 16, 1, 1),
-                (8, 64, 56, 56), (12, 130, 27, 29), (16, 512, 7, 7), (32, 130, 27, 29)]
+                (8, 64, 56, 56), (12, 130, 27, 29), (16, 512, 7, 7), (32, 130, 27, 29),
+                (32, 256, 14, 14), (32, 512, 7, 7), (32, 200, 14, 14)]
 
 
 @pytest.mark.parametrize("B,K,Ho,Wo", OUTPUT_CASES)

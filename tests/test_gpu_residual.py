@@ -37,9 +37,11 @@ def _run(path, x, w, pad, bias=None, relu=0, res=None):
 
 
 # batch 1 / small: lane-parallel output transform; (8,64,64,56) and
-# (32,64,64,24): tile-block (the latter with 8-byte row segments)
+# (32,64,64,24): tile-block (the latter with 8-byte row segments);
+# (32,128,256,14) and (32,64,512,7): the image-block form (three-pass) with a
+# 16-byte aligned residual, the tile-block form with the offset one
 CASES = [(1, 64, 64, 56, 1), (8, 64, 64, 56, 1), (32, 64, 64, 24, 1), (2, 48, 40, 13, 1),
-         (3, 20, 36, 17, 2)]
+         (3, 20, 36, 17, 2), (32, 128, 256, 14, 1), (32, 64, 512, 7, 1)]
 
 
 @pytest.mark.parametrize("aligned", [True, False], ids=["aligned", "offset2"])
