@@ -188,10 +188,10 @@ def pmc_workload(runs, reps, torch):
 # GEMM, belong to their stage's family. The roofline's dominant kernel is the
 # family with the largest summed time per step.
 KERNEL_FAMILY = {"input_transform_kernel": ("input_transform_kernel", "input_lp_kernel",
-                                            "input_nhwc_kernel"),
+                                            "input_nhwc_kernel", "input_run_kernel"),
                  "wgemm": ("wgemm_kernel", "wgemm_lds_kernel", "wgemm_block_kernel"),
                  "output_transform_kernel": ("output_transform_kernel", "output_lp_kernel",
-                                             "output_nhwc_kernel"),
+                                             "output_nhwc_kernel", "output_image_kernel"),
                  "in_gemm_kernel": ("in_gemm_kernel",)}
 FAMILY_OF_KIND = {0: "input_transform_kernel", 1: "wgemm", 2: "output_transform_kernel"}
 
